@@ -1,0 +1,133 @@
+/*
+ * ullm_hip.h -- C ABI of the MI355X (gfx950) attention path for uLLM.
+ *
+ * These entry points replace the attention ops that the reference's Metal
+ * backend encodes inside `GpuForward` (crates/ullm-metal/src/forward.rs).
+ * A Rust `ullm-hip` crate binds them with `extern "C"` and keeps the
+ * `GpuForward::{new, forward, forward_batch}` surface unchanged.
+ *
+ * Conventions shared by every entry point:
+ *  - All tensor pointers are DEVICE pointers owned by the caller.
+ *  - `stream` is a hipStream_t (NULL = the default stream).  Calls are
+ *    asynchronous on that stream; nothing synchronises the device.
+ *  - The return value is a status: ULLM_HIP_OK (0) or a negative code.  The
+ *    thread-local message of the last failure is ullm_hip_last_error().
+ *    The Rust side maps ULLM_HIP_E_INVALID to `Error::Format` and
+ *    ULLM_HIP_E_UNSUPPORTED to `Error::Unsupported`
+ *    (crates/ullm-core/src/error.rs:11-18), as forward.rs:369-380 does for
+ *    dtypes it cannot encode.
+ *  - KV cache layout is the reference's, token-major per layer
+ *    (crates/ullm-model/src/lib.rs:184-185, forward.rs:355-356):
+ *    position t of kv head j starts at element  t*kv_stride + j*head_dim
+ *    from the layer base, kv_stride = n_kv_head*head_dim for a dense cache.
+ *    Element type is f32, f16 or bf16 (ullm_hip_dtype).
+ *  - The library keeps no global mutable state besides the error string;
+ *    calls on different streams may overlap if their buffers do not.
+ */
+#ifndef ULLM_HIP_H
+#define ULLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    ULLM_HIP_OK = 0,
+    ULLM_HIP_E_INVALID = -1,     /* bad shape / argument                */
+    ULLM_HIP_E_UNSUPPORTED = -2, /* dtype / head_dim combination absent */
+    ULLM_HIP_E_HIP = -3,         /* HIP runtime error                   */
+    ULLM_HIP_E_WORKSPACE = -4    /* workspace missing or too small      */
+};
+
+typedef enum { ULLM_DT_F32 = 0, ULLM_DT_F16 = 1, ULLM_DT_BF16 = 2 } ullm_hip_dtype;
+
+/* Library version string, e.g. "ullm-hip 0.1.0 gfx950". */
+const char *ullm_hip_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *ullm_hip_last_error(void);
+
+/* Bytes of device workspace ullm_hip_attn_decode needs for this shape.
+ * max_len is the largest seq_len the call will see.  The workspace holds
+ * split-KV partials plus a counter area that must be ZERO before its first
+ * use; every completed decode call leaves the counters at zero again, so
+ * one hipMemset at allocation suffices.  One workspace serves one stream at
+ * a time. */
+size_t ullm_hip_decode_workspace_bytes(int batch, int n_head, int n_kv_head, int head_dim,
+                                       int max_len, int window);
+
+/* Single-query GQA decode attention over the resident KV cache.
+ * Replaces attn_scores/attn_softmax/attn_output
+ * (crates/ullm-metal/src/forward.rs:449-466, shader.metal:944-1021) and
+ * computes what the CPU reference computes at
+ * crates/ullm-model/src/lib.rs:911-938 (full) and :1180-1208 (windowed):
+ *   for each sequence b and query head h, kv head j = h / (n_head/n_kv_head):
+ *     keys  start..len-1,  len = seq_lens[b] (= pos+1),
+ *     start = (window > 0 && len > window) ? len - window : 0
+ *     out[b,h,:] = softmax_t(scale * q[b,h,:].K[t,j,:]) . V[t,j,:]
+ * q:        [batch][n_head][head_dim] f32 (after bias, Q-norm and RoPE)
+ * k_cache,
+ * v_cache:  layer base of sequence 0; sequence b starts seq_stride elements
+ *           after sequence b-1 (ignored when batch == 1)
+ * seq_lens: DEVICE int32[batch], each in 1..max_len
+ * max_len:  host-side upper bound of seq_lens (sizes the split-KV grid)
+ * out:      [batch][n_head][head_dim] f32
+ * head_dim in {64, 128, 256}; n_head % n_kv_head == 0. */
+int ullm_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype,
+                         int64_t kv_stride, int64_t seq_stride, const int32_t *seq_lens,
+                         int max_len, int window, int batch, int n_head, int n_kv_head,
+                         int head_dim, float scale, float *out, void *workspace,
+                         size_t workspace_bytes, void *stream);
+
+/* Causal multi-token prefill attention on MFMA.
+ * Replaces attn_flash_batch (crates/ullm-metal/src/forward.rs:855-858,
+ * :1116-1147; shader.metal:1030-1074) and computes what the CPU reference
+ * computes at crates/ullm-model/src/lib.rs:1061-1087: query row s sits at
+ * pos = start_pos + s and attends keys start..pos, where start is 0, or
+ * pos+1-window when window > 0 and pos+1 > window (a sliding-window layer,
+ * shader.metal:1051).  The cache must already hold positions
+ * 0..start_pos+S-1 (lib.rs:1056-1058).
+ * q:     [S][n_head*head_dim] in `dtype` (after Q-norm and RoPE)
+ * cache: `dtype` (f16 or bf16; the same dtype as q)
+ * out:   [S][n_head*head_dim] f32
+ * head_dim in {64, 128, 256}.  For bf16, P.V runs in f16 (V is widened to
+ * f16 on chip), so |V| must stay below 65504. */
+int ullm_hip_attn_prefill(const void *q, const void *k_cache, const void *v_cache, int dtype,
+                          int64_t kv_stride, int S, int start_pos, int window, int n_head,
+                          int n_kv_head, int head_dim, float scale, float *out, void *stream);
+
+/* Fills host memory `cs` ([n_pos][rotary_dim/2][2] f32, (cos, sin)) with the
+ * RoPE angles of the CPU reference: freq_i = theta.powf(2i/rd).recip() and
+ * (sin, cos) = (pos*freq_i).sin_cos() in f32
+ * (crates/ullm-model/src/math.rs:116-161).  The same table serves NeoX and
+ * interleaved RoPE.  Upload it once per model, like GpuForward::new uploads
+ * weights. */
+int ullm_hip_rope_table(float *cs, int n_pos, int rotary_dim, float theta);
+
+/* Fused Q/K/V preparation and KV-cache append for `rows` tokens at positions
+ * start_pos..start_pos+rows-1.  Replaces the bias / rmsnorm_heads / rope
+ * dispatches (forward.rs:416-447 decode, :799-853 prefill;
+ * shader.metal:828-941) and computes lib.rs:1021-1058 (:877-914 for one row):
+ *   q += q_bias; k += k_bias; v += v_bias          (each optional)
+ *   per-head RMSNorm of q with q_norm, of k with k_norm (optional, eps)
+ *   RoPE of q and k (rope_neox != 0: rotate-half, else interleaved) over the
+ *   first rotary_dim dims of each head, using the table from
+ *   ullm_hip_rope_table (rope_cs: DEVICE, rope_n_pos >= start_pos+rows)
+ *   q_out = q (q_dtype), K/V rows stored into the cache (kv_dtype).
+ * q_in/k_in/v_in: [rows][n_head*head_dim] / [rows][n_kv_head*head_dim] f32.
+ * q_out may alias q_in when q_dtype is f32. */
+int ullm_hip_qkv_append(const float *q_in, const float *k_in, const float *v_in,
+                        const float *q_bias, const float *k_bias, const float *v_bias,
+                        const float *q_norm, const float *k_norm, float eps,
+                        const float *rope_cs, int rope_n_pos, int rope_neox, int rotary_dim,
+                        int rows, int start_pos, int n_head, int n_kv_head, int head_dim,
+                        void *q_out, int q_dtype, void *k_cache, void *v_cache, int kv_dtype,
+                        int64_t kv_stride, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ULLM_HIP_H */

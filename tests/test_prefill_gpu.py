@@ -1,0 +1,101 @@
+"""Causal prefill attention (MFMA) on the GPU against the CPU oracle.
+
+The oracle computes a sample of query rows (first rows, block and tile
+boundaries, the last row, random rows) for every head; at full size the
+GPU result is also checked row-wise against the GPU decode kernel, the
+reference's own "batched prefill == per-token" invariant
+(crates/ullm-model/src/lib.rs:1348-1382).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as ora
+from tests.helpers import assert_close
+from ullm_amd import attention as A
+from ullm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+DT = {"f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def sample_rows(S, seed, extra=24):
+    rows = {0, 1, 2, 31, 32, 63, 64, 127, 128, 129, S - 2, S - 1}
+    rng = np.random.default_rng(seed)
+    rows |= set(int(x) for x in rng.integers(0, S, size=extra))
+    return sorted(r for r in rows if 0 <= r < S)
+
+
+def run_case(dev, dtype, S, H, Hk, D, start_pos=0, window=0, seed=1, rows=None):
+    dt = DT[dtype]
+    kv_len = start_pos + S
+    print(f"[prefill] {dtype} S{S} sp{start_pos} H{H} Hk{Hk} D{D} win={window}", flush=True)
+    q = synth.randn(seed, 1, (S, H * D), dt).to(dev)
+    k = synth.randn(seed, 2, (kv_len, Hk * D), dt).to(dev)
+    v = synth.randn(seed, 3, (kv_len, Hk * D), dt).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    out = A.attn_prefill(q, k, v, H, Hk, D, start_pos=start_pos, window=window, scale=scale)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    rows = sample_rows(S, seed) if rows is None else rows
+    ref = ora.attn_prefill(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                           v.float().cpu().numpy(), S, start_pos, H, Hk, D, scale,
+                           window=window, rows=rows)
+    assert_close(out[rows], ref[rows], what=f"rows {rows[:6]}..")
+    return q, k, v, out
+
+
+def test_cfg3_qwen3_4b_bf16_2048(dev):
+    run_case(dev, "bf16", 2048, 32, 8, 128, seed=3)
+
+
+def test_cfg4_gemma3_f16_1024_window(dev):
+    run_case(dev, "f16", 1024, 8, 4, 256, window=1024, seed=4)
+
+
+@pytest.mark.parametrize("S,window", [(1536, 512), (700, 100), (300, 1)])
+def test_window_masking(dev, S, window):
+    run_case(dev, "f16", S, 8, 4, 128, window=window, seed=5)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_dtypes_head_dims(dev, dtype, D):
+    run_case(dev, dtype, 200, 4, 2, D, seed=6, rows=list(range(200)))
+
+
+@pytest.mark.parametrize("S", [1, 2, 31, 33, 127, 129, 257])
+def test_ragged_lengths(dev, S):
+    run_case(dev, "bf16", S, 8, 2, 128, seed=7, rows=list(range(S)))
+
+
+@pytest.mark.parametrize("start_pos", [1, 100, 1000])
+def test_chunked_prefill_start_pos(dev, start_pos):
+    run_case(dev, "bf16", 300, 8, 4, 128, start_pos=start_pos, seed=8)
+
+
+@pytest.mark.parametrize("H,Hk", [(6, 1), (12, 2), (8, 8), (10, 5)])
+def test_gqa(dev, H, Hk):
+    run_case(dev, "f16", 260, H, Hk, 64, seed=9, rows=list(range(260)))
+
+
+def test_prefill_rows_match_decode_full_size(dev):
+    """cfg3 at full size: every 97th row equals the decode kernel at that pos."""
+    S, H, Hk, D = 2048, 32, 8, 128
+    q, k, v, out = run_case(dev, "bf16", S, H, Hk, D, seed=10, rows=[0, S - 1])
+    rows = list(range(0, S, 97)) + [S - 1]
+    qd = q[rows].float().view(len(rows), H, D).contiguous()
+    lens = torch.tensor([r + 1 for r in rows], dtype=torch.int32, device=dev)
+    dec = A.attn_decode(qd, k, v, lens, S, Hk, seq_stride=0)
+    torch.cuda.synchronize()
+    assert_close(out[rows], dec.view(len(rows), -1).cpu().numpy(), what="prefill vs decode")
+
+
+def test_rejects_f32(dev):
+    q = torch.zeros(4, 128, device=dev)
+    with pytest.raises(A.L.UllmHipError) as e:
+        A.attn_prefill(q, q, q, 1, 1, 128)
+    assert e.value.code == A.L.E_UNSUPPORTED

@@ -1,0 +1,254 @@
+"""Torch-tensor front end of the C ABI, and `GpuAttention`, the attention
+part of the reference's `GpuForward` (crates/ullm-metal/src/forward.rs).
+
+Every op here is a thin call into libullm_hip.so; torch supplies device
+memory and the current HIP stream and nothing else.  There is no CPU or
+PyTorch fallback: without the library or a GPU the calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+
+_DT = {torch.float32: L.DT_F32, torch.float16: L.DT_F16, torch.bfloat16: L.DT_BF16}
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise L.UllmHipError(L.E_UNSUPPORTED, f"dtype {t.dtype} not supported") from None
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    s = torch.cuda.current_stream() if stream is None else stream
+    return C.c_void_p(s.cuda_stream)
+
+
+def _need_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise L.UllmHipError(L.E_INVALID, "tensors must live on the GPU")
+
+
+def decode_workspace_bytes(batch, n_head, n_kv_head, head_dim, max_len, window=0) -> int:
+    return int(L.lib().ullm_hip_decode_workspace_bytes(batch, n_head, n_kv_head, head_dim,
+                                                       max_len, window))
+
+
+def new_decode_workspace(batch, n_head, n_kv_head, head_dim, max_len, window=0, device="cuda"):
+    """Zeroed workspace for attn_decode (the counter area must start at zero)."""
+    n = max(decode_workspace_bytes(batch, n_head, n_kv_head, head_dim, max_len, window), 256)
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def attn_decode(q, k_cache, v_cache, seq_lens, max_len, n_kv_head, *, window=0, scale=None,
+                kv_stride=None, seq_stride=0, out=None, workspace=None, stream=None):
+    """Single-query GQA decode attention (lib.rs:911-938 / :1180-1208).
+
+    q: [B, n_head, D] f32.  k_cache/v_cache: layer base (f32/f16/bf16) with
+    `kv_stride` elements per position (default n_kv_head*D) and `seq_stride`
+    between sequences.  seq_lens: int32 [B] on the GPU (= pos + 1).
+    """
+    B, H, D = q.shape
+    _need_cuda(q, k_cache, v_cache, seq_lens)
+    if q.dtype != torch.float32 or not q.is_contiguous():
+        raise L.UllmHipError(L.E_INVALID, "q must be contiguous f32 [B, n_head, head_dim]")
+    if seq_lens.dtype != torch.int32 or seq_lens.numel() != B:
+        raise L.UllmHipError(L.E_INVALID, "seq_lens must be int32 [B]")
+    if kv_stride is None:
+        kv_stride = n_kv_head * D
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty(B, H, D, dtype=torch.float32, device=q.device)
+    if workspace is None:
+        workspace = new_decode_workspace(B, H, n_kv_head, D, max_len, window, q.device)
+    rc = L.lib().ullm_hip_attn_decode(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _dt(k_cache), kv_stride, seq_stride,
+        _ptr(seq_lens), max_len, window, B, H, n_kv_head, D, float(scale), _ptr(out),
+        _ptr(workspace), workspace.numel(), _stream(stream))
+    L.check(rc)
+    return out
+
+
+def attn_prefill(q, k_cache, v_cache, n_head, n_kv_head, head_dim, *, start_pos=0, window=0,
+                 scale=None, kv_stride=None, out=None, stream=None):
+    """Causal prefill attention on MFMA (lib.rs:1061-1087).
+
+    q: [S, n_head*head_dim] in the cache dtype (f16/bf16); the cache already
+    holds positions 0..start_pos+S-1.  Returns [S, n_head*head_dim] f32.
+    """
+    S = q.shape[0]
+    _need_cuda(q, k_cache, v_cache)
+    if not q.is_contiguous() or q.numel() != S * n_head * head_dim:
+        raise L.UllmHipError(L.E_INVALID, "q must be contiguous [S, n_head*head_dim]")
+    if q.dtype != k_cache.dtype or q.dtype != v_cache.dtype:
+        raise L.UllmHipError(L.E_INVALID, "q and cache dtypes differ")
+    if kv_stride is None:
+        kv_stride = n_kv_head * head_dim
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    if out is None:
+        out = torch.empty(S, n_head * head_dim, dtype=torch.float32, device=q.device)
+    rc = L.lib().ullm_hip_attn_prefill(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _dt(q), kv_stride, S, start_pos, window, n_head,
+        n_kv_head, head_dim, float(scale), _ptr(out), _stream(stream))
+    L.check(rc)
+    return out
+
+
+def rope_table(n_pos: int, rotary_dim: int, theta: float, device="cuda") -> torch.Tensor:
+    """(cos, sin) table [n_pos, rotary_dim/2, 2] with the reference formula,
+    computed on the host by the library and uploaded."""
+    host = torch.empty(n_pos, rotary_dim // 2, 2, dtype=torch.float32)
+    L.check(L.lib().ullm_hip_rope_table(C.c_void_p(host.data_ptr()), n_pos, rotary_dim,
+                                        float(theta)))
+    return host.to(device) if device != "cpu" else host
+
+
+def qkv_append(q, k, v, k_cache, v_cache, rope_cs, *, start_pos, n_head, n_kv_head, head_dim,
+               rotary_dim=None, neox=True, q_norm=None, k_norm=None, eps=1e-6, q_bias=None,
+               k_bias=None, v_bias=None, q_out=None, q_dtype=None, kv_stride=None, stream=None):
+    """Fused bias + Q/K RMSNorm + RoPE + KV append (lib.rs:1021-1058).
+
+    q: [rows, n_head*D] f32, k/v: [rows, n_kv_head*D] f32.  K/V land in the
+    cache at positions start_pos..; returns q_out ([rows, n_head*D], q_dtype).
+    """
+    rows = q.shape[0]
+    _need_cuda(q, k, v, k_cache, v_cache, rope_cs)
+    for t in (q, k, v):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise L.UllmHipError(L.E_INVALID, "q/k/v must be contiguous f32")
+    if rotary_dim is None:
+        rotary_dim = head_dim
+    if q_dtype is None:
+        q_dtype = torch.float32
+    if q_out is None:
+        q_out = torch.empty(rows, n_head * head_dim, dtype=q_dtype, device=q.device)
+    if kv_stride is None:
+        kv_stride = n_kv_head * head_dim
+    rc = L.lib().ullm_hip_qkv_append(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(q_bias), _ptr(k_bias), _ptr(v_bias), _ptr(q_norm),
+        _ptr(k_norm), float(eps), _ptr(rope_cs), rope_cs.shape[0], int(bool(neox)), rotary_dim,
+        rows, start_pos, n_head, n_kv_head, head_dim, _ptr(q_out), _DT[q_out.dtype],
+        _ptr(k_cache), _ptr(v_cache), _dt(k_cache), kv_stride, _stream(stream))
+    L.check(rc)
+    return q_out
+
+
+@dataclass
+class AttnParams:
+    """The attention fields of the reference's GpuParams (forward.rs:23-51)."""
+
+    n_layer: int
+    n_head: int
+    n_kv_head: int
+    head_dim: int
+    n_ctx: int
+    rope_theta: float = 10000.0
+    eps: float = 1e-6
+    rope_neox: bool = True
+    rotary_dim: Optional[int] = None
+    sliding_window: int = 0
+    kv_dtype: torch.dtype = torch.float16
+
+
+class GpuAttention:
+    """Resident KV cache + the attention ops of one model, on one GPU.
+
+    Mirrors what `GpuForward` owns and does for attention: the cache is
+    `[n_layer][n_ctx][n_kv_head*head_dim]` (forward.rs:355-356), per-token
+    decode appends then attends (forward.rs:414-466), batched prefill
+    appends all rows then runs one causal attention (forward.rs:799-858),
+    and Gemma-style local layers (`l % 6 != 5`) use the sliding window
+    (forward.rs:450-454, :857).  Like GpuForward it is not thread-safe:
+    one caller at a time (forward.rs:221-225).
+    """
+
+    def __init__(self, p: AttnParams, device="cuda"):
+        if p.n_head % p.n_kv_head:
+            raise L.UllmHipError(L.E_INVALID, "n_head must be a multiple of n_kv_head")
+        self.p = p
+        self.device = torch.device(device)
+        self.rotary_dim = p.rotary_dim or p.head_dim
+        self.kv_dim = p.n_kv_head * p.head_dim
+        self.scale = 1.0 / math.sqrt(p.head_dim)
+        shape = (p.n_layer, p.n_ctx, self.kv_dim)
+        self.key_cache = torch.zeros(shape, dtype=p.kv_dtype, device=self.device)
+        self.val_cache = torch.zeros(shape, dtype=p.kv_dtype, device=self.device)
+        self.rope_cs = rope_table(p.n_ctx, self.rotary_dim, p.rope_theta, device=self.device)
+        self.workspace = new_decode_workspace(1, p.n_head, p.n_kv_head, p.head_dim, p.n_ctx,
+                                              0, self.device)
+        self._len = torch.zeros(1, dtype=torch.int32, device=self.device)
+
+    def supports_batched_prefill(self) -> bool:
+        """Prefill runs on MFMA for f16/bf16 caches; an f32 cache takes the
+        split-KV kernel with one ragged sequence per query row."""
+        return True
+
+    def _window(self, layer: int) -> int:
+        p = self.p
+        return p.sliding_window if (p.sliding_window > 0 and layer % 6 != 5) else 0
+
+    def _append(self, layer, q, k, v, start_pos, q_dtype, norms, biases):
+        p = self.p
+        qn, kn = norms
+        qb, kb, vb = biases
+        return qkv_append(q, k, v, self.key_cache[layer], self.val_cache[layer], self.rope_cs,
+                          start_pos=start_pos, n_head=p.n_head, n_kv_head=p.n_kv_head,
+                          head_dim=p.head_dim, rotary_dim=self.rotary_dim, neox=p.rope_neox,
+                          q_norm=qn, k_norm=kn, eps=p.eps, q_bias=qb, k_bias=kb, v_bias=vb,
+                          q_dtype=q_dtype)
+
+    def forward(self, layer: int, q, k, v, pos: int, q_norm=None, k_norm=None, q_bias=None,
+                k_bias=None, v_bias=None):
+        """Decode one token: q [n_head*D], k/v [n_kv_head*D] f32 projections.
+        Returns the attention output [n_head*D] f32."""
+        p = self.p
+        if not 0 <= pos < p.n_ctx:
+            raise L.UllmHipError(L.E_INVALID, f"pos {pos} outside the context")
+        qr = self._append(layer, q.view(1, -1), k.view(1, -1), v.view(1, -1), pos,
+                          torch.float32, (q_norm, k_norm), (q_bias, k_bias, v_bias))
+        self._len.fill_(pos + 1)
+        out = attn_decode(qr.view(1, p.n_head, p.head_dim), self.key_cache[layer],
+                          self.val_cache[layer], self._len, pos + 1, p.n_kv_head,
+                          window=self._window(layer), scale=self.scale,
+                          workspace=self.workspace)
+        return out.view(-1)
+
+    def forward_batch(self, layer: int, q, k, v, start_pos: int = 0, q_norm=None, k_norm=None,
+                      q_bias=None, k_bias=None, v_bias=None):
+        """Prefill S tokens at start_pos..: q [S, n_head*D], k/v [S, kv_dim] f32.
+        Returns the attention output [S, n_head*D] f32."""
+        p = self.p
+        S = q.shape[0]
+        if start_pos + S > p.n_ctx:
+            raise L.UllmHipError(L.E_INVALID, "prompt exceeds the context")
+        if p.kv_dtype == torch.float32:
+            qr = self._append(layer, q, k, v, start_pos, torch.float32, (q_norm, k_norm),
+                              (q_bias, k_bias, v_bias))
+            lens = torch.arange(start_pos + 1, start_pos + S + 1, dtype=torch.int32,
+                                device=self.device)
+            ws = new_decode_workspace(S, p.n_head, p.n_kv_head, p.head_dim, start_pos + S,
+                                      self._window(layer), self.device)
+            out = attn_decode(qr.view(S, p.n_head, p.head_dim), self.key_cache[layer],
+                              self.val_cache[layer], lens, start_pos + S, p.n_kv_head,
+                              window=self._window(layer), scale=self.scale, seq_stride=0,
+                              workspace=ws)
+            return out.view(S, -1)
+        qr = self._append(layer, q, k, v, start_pos, p.kv_dtype, (q_norm, k_norm),
+                          (q_bias, k_bias, v_bias))
+        return attn_prefill(qr, self.key_cache[layer], self.val_cache[layer], p.n_head,
+                            p.n_kv_head, p.head_dim, start_pos=start_pos,
+                            window=self._window(layer), scale=self.scale)

@@ -1,0 +1,90 @@
+// Shared helpers for the gfx950 attention kernels: element types, 16-byte
+// vector loads, conversions and the error/status plumbing of the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/ullm_hip.h"
+
+namespace ullm {
+
+// Storage tags.  Caches hold raw 16-bit patterns; conversion is explicit so
+// that bf16 and f16 never go through a compiler-chosen path.
+struct F32 { using raw = float; static constexpr int bytes = 4; };
+struct F16 { using raw = uint16_t; static constexpr int bytes = 2; };
+struct BF16 { using raw = uint16_t; static constexpr int bytes = 2; };
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float f16_lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+}
+__device__ __forceinline__ float f16_hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// Round-to-nearest-even f32 -> bf16 bits (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Widen one 16-byte chunk (4 f32 or 8 half-precision values) to f32.
+template <class T> struct Chunk;
+template <> struct Chunk<F32> {
+    static constexpr int n = 4;
+    __device__ __forceinline__ static void widen(const u32x4 &r, float *o) {
+        o[0] = __uint_as_float(r[0]); o[1] = __uint_as_float(r[1]);
+        o[2] = __uint_as_float(r[2]); o[3] = __uint_as_float(r[3]);
+    }
+};
+template <> struct Chunk<F16> {
+    static constexpr int n = 8;
+    __device__ __forceinline__ static void widen(const u32x4 &r, float *o) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) { o[2 * i] = f16_lo(r[i]); o[2 * i + 1] = f16_hi(r[i]); }
+    }
+};
+template <> struct Chunk<BF16> {
+    static constexpr int n = 8;
+    __device__ __forceinline__ static void widen(const u32x4 &r, float *o) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) { o[2 * i] = bf16_lo(r[i]); o[2 * i + 1] = bf16_hi(r[i]); }
+    }
+};
+
+__device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
+// Streaming load: the KV cache is read exactly once per decode call, so keep
+// it from displacing reusable lines.
+__device__ __forceinline__ u32x4 ld16_stream(const void *p) {
+    return __builtin_nontemporal_load((const u32x4 *)p);
+}
+
+// Host-side status plumbing -------------------------------------------------
+int set_error(int code, const char *fmt, ...);
+inline int check_hip(hipError_t e, const char *what) {
+    if (e != hipSuccess) return set_error(ULLM_HIP_E_HIP, "%s: %s", what, hipGetErrorString(e));
+    return ULLM_HIP_OK;
+}
+inline int dtype_bytes(int dt) { return dt == ULLM_DT_F32 ? 4 : 2; }
+inline bool dtype_ok(int dt) { return dt == ULLM_DT_F32 || dt == ULLM_DT_F16 || dt == ULLM_DT_BF16; }
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace ullm

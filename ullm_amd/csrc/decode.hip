@@ -1,0 +1,379 @@
+// Split-KV single-query GQA decode attention for gfx950.
+//
+// Computes, for every sequence b and query head h (kv head h / kv_mul),
+//   out[b,h] = softmax_t(scale * q[b,h] . K[t]) . V[t],  t in start..len-1
+// which is the CPU reference loop crates/ullm-model/src/lib.rs:916-938
+// (windowed start: lib.rs:1183-1186).
+//
+// Design (HBM-bound stream):
+//  * One workgroup owns (sequence b, a group of G query heads that share one
+//    kv head, a chunk of keys).  Each K/V row is loaded ONCE, with 16-byte
+//    loads, and serves all G heads from registers (the Metal path re-reads
+//    K/V per query head, shader.metal:957-964, :1014-1020).
+//  * A row of D elements is spread over LPT = D/EPL lanes (EPL elements per
+//    16-byte load); a wave therefore covers TPW = 64/LPT consecutive keys per
+//    load instruction.  Each such lane group runs its own online softmax over
+//    its keys (tiles of TT keys, one max/rescale per tile), so the only
+//    cross-lane traffic in the stream is the LPT-lane dot-product sum (DPP).
+//  * Lane groups merge by shuffles, waves merge through LDS, and chunks
+//    (splits) merge in the same launch: every workgroup publishes its
+//    (m, l, acc) partial, and the last one to arrive for a (b, head group),
+//    found with an agent-scope counter, combines them and writes `out`.
+//  * Softmax runs in the exp2 domain: q is pre-multiplied by scale*log2(e).
+#include "common.hpp"
+#include "wave.hpp"
+
+namespace ullm {
+
+constexpr int kDecodeWaves = 8;
+
+template <class T, int D, int G>
+struct DecodeCfg {
+    static constexpr int EPL = Chunk<T>::n;
+    static constexpr int LPT = D / EPL;
+    static constexpr int TPW = 64 / LPT;
+    static constexpr int NW = kDecodeWaves;
+    static constexpr int NLG = NW * TPW;                 // lane groups per workgroup
+    static constexpr int TT = (G * EPL <= 48) ? 8 : 4;   // keys per lane group per tile
+    static_assert(LPT >= 1 && LPT <= 64 && (LPT & (LPT - 1)) == 0, "bad lanes per key");
+};
+
+template <class T, int D, int G>
+__global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
+    const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
+    int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
+    int n_head, int kv_mul, int n_groups, int chunk, int splits, float qscale,
+    float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc,
+    uint32_t *__restrict__ counters) {
+    using C = DecodeCfg<T, D, G>;
+    constexpr int EPL = C::EPL, LPT = C::LPT, TPW = C::TPW, NW = C::NW, NLG = C::NLG, TT = C::TT;
+    constexpr int EB = T::bytes;
+
+    const int split = blockIdx.x, grp = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = lane % LPT, lg = wave * TPW + lane / LPT;
+    const int head0 = grp * G, kvh = head0 / kv_mul;
+
+    const int len = seq_lens[b];
+    const int start = (window > 0 && len > window) ? len - window : 0;
+    const int c0 = start + split * chunk;
+    const int c1 = min(c0 + chunk, len);
+
+    // q slice of this lane, pre-scaled into the exp2 domain.
+    float qf[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float *qp = q + ((int64_t)b * n_head + head0 + g) * D + sub * EPL;
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4) {
+            f32x4 v = *(const f32x4 *)(qp + e);
+            qf[g][e] = v[0] * qscale; qf[g][e + 1] = v[1] * qscale;
+            qf[g][e + 2] = v[2] * qscale; qf[g][e + 3] = v[3] * qscale;
+        }
+    }
+
+    float m[G], l[G], acc[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY; l[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) acc[g][e] = 0.f;
+    }
+
+    const int64_t row_bytes = kv_stride * EB;
+    const char *kbase = kc + (int64_t)b * seq_stride * EB + ((int64_t)kvh * D + sub * EPL) * EB;
+    const char *vbase = vc + (int64_t)b * seq_stride * EB + ((int64_t)kvh * D + sub * EPL) * EB;
+
+    for (int base = c0; base < c1; base += NLG * TT) {
+        u32x4 kr[TT], vr[TT];
+        bool ok[TT];
+#pragma unroll
+        for (int i = 0; i < TT; i++) {
+            const int t = base + lg + NLG * i;
+            ok[i] = t < c1;
+            kr[i] = ok[i] ? ld16_stream(kbase + (int64_t)t * row_bytes) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < TT; i++) {
+            const int t = base + lg + NLG * i;
+            vr[i] = ok[i] ? ld16_stream(vbase + (int64_t)t * row_bytes) : u32x4{0, 0, 0, 0};
+        }
+        float s[G][TT];
+#pragma unroll
+        for (int i = 0; i < TT; i++) {
+            float kf[EPL];
+            Chunk<T>::widen(kr[i], kf);
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) d += qf[g][e] * kf[e];
+                d = group_sum<LPT>(d);
+                s[g][i] = ok[i] ? d : -INFINITY;
+            }
+        }
+        float pv[G][TT], corr[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float mt = s[g][0];
+#pragma unroll
+            for (int i = 1; i < TT; i++) mt = fmaxf(mt, s[g][i]);
+            const float mn = fmaxf(m[g], mt);
+            const float mu = (mn == -INFINITY) ? 0.f : mn;  // all masked so far
+            corr[g] = exp2f(m[g] - mu);
+            float ps = 0.f;
+#pragma unroll
+            for (int i = 0; i < TT; i++) { pv[g][i] = exp2f(s[g][i] - mu); ps += pv[g][i]; }
+            l[g] = l[g] * corr[g] + ps;
+            m[g] = mn;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) acc[g][e] *= corr[g];
+        }
+#pragma unroll
+        for (int i = 0; i < TT; i++) {
+            float vf[EPL];
+            Chunk<T>::widen(vr[i], vf);
+#pragma unroll
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int e = 0; e < EPL; e++) acc[g][e] += pv[g][i] * vf[e];
+        }
+    }
+
+    // Merge the lane groups of this wave (lanes sub, sub+LPT, ...).
+#pragma unroll
+    for (int off = LPT; off < 64; off <<= 1) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float mo = __shfl_xor(m[g], off, 64);
+            const float lo = __shfl_xor(l[g], off, 64);
+            const float mn = fmaxf(m[g], mo);
+            const float mu = (mn == -INFINITY) ? 0.f : mn;
+            const float a = exp2f(m[g] - mu), c = exp2f(mo - mu);
+            l[g] = l[g] * a + lo * c;
+            m[g] = mn;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) {
+                const float ao = __shfl_xor(acc[g][e], off, 64);
+                acc[g][e] = acc[g][e] * a + ao * c;
+            }
+        }
+    }
+
+    // Merge the waves through LDS.
+    __shared__ float sm_ml[NW][G][2];
+    __shared__ float sm_acc[NW][G][D];
+    __shared__ int sm_last;
+    if (lane < LPT) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            if (lane == 0) { sm_ml[wave][g][0] = m[g]; sm_ml[wave][g][1] = l[g]; }
+#pragma unroll
+            for (int e = 0; e < EPL; e++) sm_acc[wave][g][sub * EPL + e] = acc[g][e];
+        }
+    }
+    __syncthreads();
+
+    const int64_t unit = (int64_t)b * n_groups + grp;
+    for (int idx = tid; idx < G * D; idx += NW * 64) {
+        const int g = idx / D, d = idx % D;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; w++) mx = fmaxf(mx, sm_ml[w][g][0]);
+        const float mu = (mx == -INFINITY) ? 0.f : mx;
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float c = exp2f(sm_ml[w][g][0] - mu);
+            num += sm_acc[w][g][d] * c;
+            den += sm_ml[w][g][1] * c;
+        }
+        if (splits == 1) {
+            out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
+        } else {
+            ws_acc[(unit * splits + split) * (G * D) + idx] = num;
+            if (d == 0) {
+                ws_ml[((unit * splits + split) * G + g) * 2 + 0] = mx;
+                ws_ml[((unit * splits + split) * G + g) * 2 + 1] = den;
+            }
+        }
+    }
+    if (splits == 1) return;
+
+    // Publish the partial; the last workgroup of this unit merges all splits.
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev = atomicAdd(&counters[unit], 1u);
+        sm_last = (prev == (uint32_t)(splits - 1));
+    }
+    __syncthreads();
+    if (!sm_last) return;
+    __threadfence();
+
+    const float *mlu = ws_ml + unit * splits * G * 2;
+    const float *accu = ws_acc + unit * splits * (G * D);
+    for (int idx = tid; idx < G * D; idx += NW * 64) {
+        const int g = idx / D, d = idx % D;
+        float mx = -INFINITY;
+        for (int sp = 0; sp < splits; sp++) mx = fmaxf(mx, mlu[(sp * G + g) * 2]);
+        const float mu = (mx == -INFINITY) ? 0.f : mx;
+        float num = 0.f, den = 0.f;
+        for (int sp = 0; sp < splits; sp++) {
+            const float c = exp2f(mlu[(sp * G + g) * 2] - mu);
+            num += accu[sp * (G * D) + idx] * c;
+            den += mlu[(sp * G + g) * 2 + 1] * c;
+        }
+        out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
+    }
+    if (tid == 0) counters[unit] = 0u;  // leave the counter ready for the next call
+}
+
+// ---------------------------------------------------------------------------
+// Host side: launch planning and dispatch.
+
+struct DecodePlan {
+    int G, n_groups, chunk, splits, nlg;
+    size_t off_ml, off_acc, bytes;
+};
+
+static int pick_group(int kv_mul) {
+    const int cands[] = {8, 6, 4, 2, 1};
+    for (int g : cands)
+        if (kv_mul % g == 0) return g;
+    return 1;
+}
+
+static int lanes_per_key(int dtype, int D) { return D / (16 / dtype_bytes(dtype)); }
+
+// Split-KV plan.  Chunks are multiples of the lane-group count so every lane
+// group gets whole keys; the split count aims at a few workgroups per CU but is
+// capped, because the last workgroup of a unit reads every split's partial.
+static DecodePlan plan_decode(int batch, int n_head, int n_kv_head, int D, int dtype, int max_len,
+                              int window) {
+    DecodePlan p{};
+    const int kv_mul = n_head / n_kv_head;
+    p.G = pick_group(kv_mul);
+    p.n_groups = n_head / p.G;
+    const int lpt = lanes_per_key(dtype, D);
+    p.nlg = kDecodeWaves * (64 / lpt);
+    const int visible = (window > 0 && max_len > window) ? window : max_len;
+    const int units = batch * p.n_groups;
+    const int target_wg = 512, max_splits = 128;
+    int splits = (target_wg + units - 1) / units;
+    if (splits > max_splits) splits = max_splits;
+    int chunk = (visible + splits - 1) / splits;
+    chunk = ((chunk + p.nlg - 1) / p.nlg) * p.nlg;
+    if (chunk < p.nlg) chunk = p.nlg;
+    p.chunk = chunk;
+    p.splits = (visible + chunk - 1) / chunk;
+    if (p.splits < 1) p.splits = 1;
+    const size_t ctr = ((size_t)units * 4 + 255) / 256 * 256;
+    const size_t ml = ((size_t)units * p.splits * p.G * 2 * 4 + 255) / 256 * 256;
+    const size_t ac = (size_t)units * p.splits * p.G * D * 4;
+    p.off_ml = ctr;
+    p.off_acc = ctr + ml;
+    p.bytes = p.splits > 1 ? ctr + ml + ac : 0;
+    return p;
+}
+
+template <class T, int D, int G>
+static void launch_decode(const DecodePlan &p, const float *q, const void *kc, const void *vc,
+                          int64_t kv_stride, int64_t seq_stride, const int32_t *lens, int window,
+                          int batch, int n_head, int kv_mul, float qscale, float *out, char *ws,
+                          hipStream_t st) {
+    dim3 grid(p.splits, p.n_groups, batch);
+    hipLaunchKernelGGL((decode_split_kernel<T, D, G>), grid, dim3(kDecodeWaves * 64), 0, st, q,
+                       (const char *)kc, (const char *)vc, kv_stride, seq_stride, lens, window,
+                       n_head, kv_mul, p.n_groups, p.chunk, p.splits, qscale, out,
+                       (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), (uint32_t *)ws);
+}
+
+template <class T, int D>
+static int dispatch_g(const DecodePlan &p, const float *q, const void *kc, const void *vc,
+                      int64_t kvs, int64_t ss, const int32_t *lens, int win, int batch, int nh,
+                      int kv_mul, float qs, float *out, char *ws, hipStream_t st) {
+    switch (p.G) {
+        case 1: launch_decode<T, D, 1>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st); break;
+        case 2: launch_decode<T, D, 2>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st); break;
+        case 4: launch_decode<T, D, 4>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st); break;
+        case 6: launch_decode<T, D, 6>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st); break;
+        case 8: launch_decode<T, D, 8>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st); break;
+        default: return set_error(ULLM_HIP_E_UNSUPPORTED, "decode: no kernel for head group %d", p.G);
+    }
+    return check_hip(hipGetLastError(), "decode launch");
+}
+
+template <class T>
+static int dispatch_d(int D, const DecodePlan &p, const float *q, const void *kc, const void *vc,
+                      int64_t kvs, int64_t ss, const int32_t *lens, int win, int batch, int nh,
+                      int kv_mul, float qs, float *out, char *ws, hipStream_t st) {
+    switch (D) {
+        case 64: return dispatch_g<T, 64>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st);
+        case 128: return dispatch_g<T, 128>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st);
+        case 256: return dispatch_g<T, 256>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st);
+        default: return set_error(ULLM_HIP_E_UNSUPPORTED, "decode: head_dim %d not in {64,128,256}", D);
+    }
+}
+
+static int validate_decode(int kv_dtype, int64_t kv_stride, int max_len, int batch, int n_head,
+                           int n_kv_head, int D) {
+    if (!dtype_ok(kv_dtype)) return set_error(ULLM_HIP_E_UNSUPPORTED, "decode: kv dtype %d", kv_dtype);
+    if (batch < 1 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head)
+        return set_error(ULLM_HIP_E_INVALID, "decode: bad heads n_head=%d n_kv_head=%d batch=%d",
+                         n_head, n_kv_head, batch);
+    if (D != 64 && D != 128 && D != 256)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "decode: head_dim %d not in {64,128,256}", D);
+    if (max_len < 1) return set_error(ULLM_HIP_E_INVALID, "decode: max_len %d < 1", max_len);
+    if (kv_stride < (int64_t)n_kv_head * D || (kv_stride * dtype_bytes(kv_dtype)) % 16)
+        return set_error(ULLM_HIP_E_INVALID,
+                         "decode: kv_stride %lld must be >= n_kv_head*head_dim and 16-byte aligned",
+                         (long long)kv_stride);
+    return ULLM_HIP_OK;
+}
+
+}  // namespace ullm
+
+using namespace ullm;
+
+extern "C" size_t ullm_hip_decode_workspace_bytes(int batch, int n_head, int n_kv_head,
+                                                  int head_dim, int max_len, int window) {
+    if (batch < 1 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || max_len < 1) return 0;
+    // The f32 cache has the most lanes per key and thus the smallest chunks:
+    // size for the largest plan over the three dtypes.
+    size_t best = 0;
+    for (int dt = 0; dt < 3; dt++) {
+        DecodePlan p = plan_decode(batch, n_head, n_kv_head, head_dim, dt, max_len, window);
+        if (p.bytes > best) best = p.bytes;
+    }
+    return best;
+}
+
+extern "C" int ullm_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache,
+                                    int kv_dtype, int64_t kv_stride, int64_t seq_stride,
+                                    const int32_t *seq_lens, int max_len, int window, int batch,
+                                    int n_head, int n_kv_head, int head_dim, float scale,
+                                    float *out, void *workspace, size_t workspace_bytes,
+                                    void *stream) {
+    int rc = validate_decode(kv_dtype, kv_stride, max_len, batch, n_head, n_kv_head, head_dim);
+    if (rc) return rc;
+    if (!q || !k_cache || !v_cache || !seq_lens || !out)
+        return set_error(ULLM_HIP_E_INVALID, "decode: null tensor pointer");
+    if (((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q) & 15)
+        return set_error(ULLM_HIP_E_INVALID, "decode: q/k_cache/v_cache must be 16-byte aligned");
+    if (batch > 1 && (seq_stride * dtype_bytes(kv_dtype)) % 16)
+        return set_error(ULLM_HIP_E_INVALID, "decode: seq_stride must be 16-byte aligned");
+    DecodePlan p = plan_decode(batch, n_head, n_kv_head, head_dim, kv_dtype, max_len, window);
+    if (p.bytes > 0 && (!workspace || workspace_bytes < p.bytes))
+        return set_error(ULLM_HIP_E_WORKSPACE, "decode: workspace of %zu bytes needed, %zu given",
+                         p.bytes, workspace_bytes);
+    const float qscale = scale * kLog2e;
+    const int kv_mul = n_head / n_kv_head;
+    hipStream_t st = (hipStream_t)stream;
+    char *ws = (char *)workspace;
+    switch (kv_dtype) {
+        case ULLM_DT_F32: return dispatch_d<F32>(head_dim, p, q, k_cache, v_cache, kv_stride, seq_stride, seq_lens, window, batch, n_head, kv_mul, qscale, out, ws, st);
+        case ULLM_DT_F16: return dispatch_d<F16>(head_dim, p, q, k_cache, v_cache, kv_stride, seq_stride, seq_lens, window, batch, n_head, kv_mul, qscale, out, ws, st);
+        default: return dispatch_d<BF16>(head_dim, p, q, k_cache, v_cache, kv_stride, seq_stride, seq_lens, window, batch, n_head, kv_mul, qscale, out, ws, st);
+    }
+}

@@ -1,0 +1,300 @@
+// Causal multi-token prefill attention on CDNA4 MFMA (gfx950).
+//
+// Computes, for query row s at pos = start_pos + s and head h (kv head
+// h / kv_mul), out[s,h] = softmax_t(scale * q[s,h] . K[t]) . V[t] over
+// t in start..pos (start = 0, or the sliding-window start) -- the CPU
+// reference loop crates/ullm-model/src/lib.rs:1061-1087, with the window rule
+// of lib.rs:1183-1186 applied per row as the Metal kernel does
+// (shader.metal:1051).
+//
+// Design:
+//  * A workgroup is 4 waves and owns BM = 128 query rows of one head; each
+//    wave owns 32 rows.  Per iteration the workgroup stages BN keys of K
+//    (as stored) and V (transposed to [d][key] and widened to f16) in LDS.
+//  * S^T = K . Q^T runs on v_mfma_f32_32x32x16_{bf16,f16}: K tiles from LDS
+//    are the A operand, the wave's Q rows stay in registers as the B operand.
+//    In the S^T accumulator every lane holds ONE query row (lane % 32) and 16
+//    keys, so the row max needs a single cross-lane exchange (lane ^ 32) and
+//    the row sum stays lane-local until the end.
+//  * The same accumulator, exponentiated and rounded to f16, IS the B operand
+//    of O^T += V^T . P^T (v_mfma_f32_32x32x16_f16): the keys' order inside a
+//    k-step is free, so V^T is read from LDS in the accumulator's key order
+//    and no register shuffle of P is needed.  P.V in f16 keeps the rounding of
+//    P at 2^-11 (bf16 would cost 2^-8 relative, beyond a 1e-3 rel-L2 budget).
+//  * Online softmax in the exp2 domain (scale*log2(e) folded into one
+//    multiply), f32 statistics and accumulators.
+//  * Tiles are ordered kv-head major and, within a kv head, longest causal
+//    row block first; blocks are dealt to the 8 XCDs so that all query heads
+//    of one kv head share one XCD's L2 (workgroup i runs on XCD i % 8).
+#include "common.hpp"
+#include "wave.hpp"
+
+namespace ullm {
+
+template <int D>
+struct PrefillCfg {
+    static constexpr int BM = 128;                    // query rows per workgroup
+    static constexpr int BN = D <= 128 ? 64 : 32;     // keys per iteration
+    static constexpr int KP = D + 8;                  // K row pitch in LDS (elements)
+    static constexpr int VP = BN + 8;                 // V^T row pitch in LDS (elements)
+    static constexpr int CPR = D / 8;                 // 16-byte chunks per key row
+    static constexpr int NCH = BN * CPR / 256;        // chunks (rows) per thread per tile
+    static constexpr int NKT = BN / 32;               // 32-key MFMA tiles per iteration
+    static constexpr int NDT = D / 32;                // 32-wide d tiles of the output
+    static constexpr int NKS = D / 16;                // 16-deep k steps of Q.K
+    static_assert(NCH >= 1 && 256 % CPR == 0, "staging map");
+};
+
+template <class T>
+__device__ __forceinline__ f32x16 mfma_qk(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
+    if constexpr (sizeof(T) && T::bytes == 2 && __is_same(T, BF16))
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t to_f16_pair(float lo, float hi) {
+    return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+}
+
+template <class T, int D>
+__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void prefill_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc,
+    const uint16_t *__restrict__ vc, int64_t kv_stride, int S, int start_pos, int window,
+    int n_head, int kv_mul, float qscale, float *__restrict__ out) {
+    using C = PrefillCfg<D>;
+    constexpr int BM = C::BM, BN = C::BN, KP = C::KP, VP = C::VP, CPR = C::CPR, NCH = C::NCH;
+    constexpr int NKT = C::NKT, NDT = C::NDT, NKS = C::NKS;
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[BN * KP];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VP];
+
+    // ---- tile assignment (XCD-aware, longest first) ----
+    const int nqb = (S + BM - 1) / BM;
+    const int total = n_head * nqb;
+    const int per_xcd = (total + 7) / 8;
+    const int t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (t >= total) return;
+    const int per_kvh = nqb * kv_mul;
+    const int kvh = t / per_kvh, r = t % per_kvh;
+    const int qb = nqb - 1 - r / kv_mul;
+    const int h = kvh * kv_mul + r % kv_mul;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 31, h2 = lane >> 5;
+    const int q0 = qb * BM, qw = q0 + wave * 32;
+    const int64_t q_dim = (int64_t)n_head * D;
+    const int kv_len = start_pos + S;
+
+    // ---- Q rows of this wave as the B operand (d = s*16 + h2*8 + j) ----
+    const int qrow = qw + c;
+    const bool row_ok = qrow < S;
+    u32x4 qreg[NKS];
+    {
+        const uint16_t *qp = q + (int64_t)(row_ok ? qrow : 0) * q_dim + (int64_t)h * D + h2 * 8;
+#pragma unroll
+        for (int s = 0; s < NKS; s++) qreg[s] = row_ok ? ld16(qp + s * 16) : u32x4{0, 0, 0, 0};
+    }
+    const int pos_row = start_pos + qrow;
+
+    // ---- key range of the workgroup and of this wave ----
+    const int wg_last = start_pos + min(q0 + BM, S) - 1;  // largest position in the block
+    const int kv_hi = wg_last + 1;
+    int kv_lo = 0;
+    if (window > 0) kv_lo = max(0, start_pos + q0 + 1 - window);
+    kv_lo = (kv_lo / BN) * BN;
+    const int w_first = start_pos + qw;                   // smallest position of the wave
+    const int w_last = start_pos + min(qw + 32, S) - 1;   // largest (may be < w_first)
+
+    f32x16 oacc[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
+    float m_run = -INFINITY, l_part = 0.f;
+
+    // ---- staging map: thread -> (column chunk cc, rows rg*NCH .. +NCH) ----
+    const int cc = tid % CPR, rg = tid / CPR;
+    const uint16_t *kg = kc + (int64_t)kvh * D + cc * 8;
+    const uint16_t *vg = vc + (int64_t)kvh * D + cc * 8;
+    u32x4 kpre[NCH], vpre[NCH];
+    auto prefetch = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            const int key = kb + rg * NCH + i;
+            const bool ok = key < kv_len;
+            kpre[i] = ok ? ld16(kg + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};
+            vpre[i] = ok ? ld16(vg + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};
+        }
+    };
+    prefetch(kv_lo);
+
+    for (int kb = kv_lo; kb < kv_hi; kb += BN) {
+        __syncthreads();  // previous tile fully consumed
+#pragma unroll
+        for (int i = 0; i < NCH; i++)
+            *(u32x4 *)&Ks[(rg * NCH + i) * KP + cc * 8] = kpre[i];
+        // V^T: element (d = cc*8 + j, key = rg*NCH + i), widened to f16.
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            float vf[NCH];
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const uint32_t w = vpre[i][j >> 1];
+                if constexpr (__is_same(T, BF16)) vf[i] = (j & 1) ? bf16_hi(w) : bf16_lo(w);
+                else vf[i] = (j & 1) ? f16_hi(w) : f16_lo(w);
+            }
+            uint16_t *dst = &Vt[(cc * 8 + j) * VP + rg * NCH];
+            if constexpr (NCH == 4) {
+                *(u32x2 *)dst = u32x2{to_f16_pair(vf[0], vf[1]), to_f16_pair(vf[2], vf[3])};
+            } else if constexpr (NCH == 2) {
+                *(uint32_t *)dst = to_f16_pair(vf[0], vf[1]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < NCH; i++) dst[i] = f32_to_f16_bits(vf[i]);
+            }
+        }
+        __syncthreads();
+        if (kb + BN < kv_hi) prefetch(kb + BN);
+
+        // Skip the MFMA work when the whole tile is masked for this wave.
+        const bool causal_dead = kb > w_last;
+        const bool window_dead = window > 0 && kb + BN - 1 < w_first + 1 - window;
+        if (causal_dead || window_dead || qw >= S) continue;
+
+        // ---- S^T = K . Q^T ----
+        f32x16 sacc[NKT];
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++) {
+            sacc[kt] = f32x16{};
+            const uint16_t *kr = &Ks[(kt * 32 + c) * KP + h2 * 8];
+#pragma unroll
+            for (int s = 0; s < NKS; s++)
+                sacc[kt] = mfma_qk<T>(*(const u32x4 *)(kr + s * 16), qreg[s], sacc[kt]);
+        }
+
+        // ---- online softmax over this tile (lane = one query row) ----
+        const bool need_mask = (kb + BN - 1 > w_first) || (window > 0 && kb < w_last + 1 - window);
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                float sv = sacc[kt][i] * qscale;
+                if (need_mask) {
+                    const int key = kb + kt * 32 + (i >> 2) * 8 + h2 * 4 + (i & 3);
+                    const bool dead = key > pos_row || (window > 0 && key <= pos_row - window);
+                    sv = dead ? -INFINITY : sv;
+                }
+                sacc[kt][i] = sv;
+                mloc = fmaxf(mloc, sv);
+            }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const float m_new = fmaxf(m_run, mloc);
+        const float mu = m_new == -INFINITY ? 0.f : m_new;
+        const float corr = exp2f(m_run - mu);
+        m_run = m_new;
+        float psum = 0.f;
+        u32x4 pk[NKT][2];
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const float p0 = exp2f(sacc[kt][ks * 8 + 2 * jj] - mu);
+                    const float p1 = exp2f(sacc[kt][ks * 8 + 2 * jj + 1] - mu);
+                    psum += p0 + p1;
+                    pk[kt][ks][jj] = to_f16_pair(p0, p1);
+                }
+        l_part = l_part * corr + psum;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) oacc[dt] *= corr;
+
+        // ---- O^T += V^T . P^T (keys in accumulator order) ----
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            const uint16_t *vr = &Vt[(dt * 32 + c) * VP + h2 * 4];
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) {
+                    const int kofs = kt * 32 + ks * 16;
+                    const u32x2 lo = *(const u32x2 *)(vr + kofs);
+                    const u32x2 hi = *(const u32x2 *)(vr + kofs + 8);
+                    const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, pk[kt][ks]),
+                        oacc[dt], 0, 0, 0);
+                }
+        }
+    }
+
+    // ---- normalise and store: lane holds row qrow, d = dt*32 + g*8 + h2*4 + 0..3 ----
+    const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    if (!row_ok) return;
+    float *op = out + (int64_t)qrow * q_dim + (int64_t)h * D + h2 * 4;
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            f32x4 v = {oacc[dt][g * 4] * inv, oacc[dt][g * 4 + 1] * inv, oacc[dt][g * 4 + 2] * inv,
+                       oacc[dt][g * 4 + 3] * inv};
+            *(f32x4 *)(op + dt * 32 + g * 8) = v;
+        }
+}
+
+template <class T, int D>
+static int launch_prefill(const void *q, const void *kc, const void *vc, int64_t kvs, int S,
+                          int sp, int win, int nh, int kv_mul, float qs, float *out,
+                          hipStream_t st) {
+    const int nqb = (S + PrefillCfg<D>::BM - 1) / PrefillCfg<D>::BM;
+    const int total = nh * nqb;
+    const int per_xcd = (total + 7) / 8;
+    hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(per_xcd * 8), dim3(256), 0, st,
+                       (const uint16_t *)q, (const uint16_t *)kc, (const uint16_t *)vc, kvs, S, sp,
+                       win, nh, kv_mul, qs, out);
+    return check_hip(hipGetLastError(), "prefill launch");
+}
+
+template <class T>
+static int dispatch_prefill(int D, const void *q, const void *kc, const void *vc, int64_t kvs,
+                            int S, int sp, int win, int nh, int kv_mul, float qs, float *out,
+                            hipStream_t st) {
+    switch (D) {
+        case 64: return launch_prefill<T, 64>(q, kc, vc, kvs, S, sp, win, nh, kv_mul, qs, out, st);
+        case 128: return launch_prefill<T, 128>(q, kc, vc, kvs, S, sp, win, nh, kv_mul, qs, out, st);
+        case 256: return launch_prefill<T, 256>(q, kc, vc, kvs, S, sp, win, nh, kv_mul, qs, out, st);
+        default: return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill: head_dim %d not in {64,128,256}", D);
+    }
+}
+
+}  // namespace ullm
+
+using namespace ullm;
+
+extern "C" int ullm_hip_attn_prefill(const void *q, const void *k_cache, const void *v_cache,
+                                     int dtype, int64_t kv_stride, int S, int start_pos,
+                                     int window, int n_head, int n_kv_head, int head_dim,
+                                     float scale, float *out, void *stream) {
+    if (dtype != ULLM_DT_F16 && dtype != ULLM_DT_BF16)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill: dtype %d (MFMA path takes f16/bf16)", dtype);
+    if (n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || S < 0 || start_pos < 0)
+        return set_error(ULLM_HIP_E_INVALID, "prefill: bad shape S=%d start_pos=%d heads=%d/%d", S,
+                         start_pos, n_head, n_kv_head);
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill: head_dim %d not in {64,128,256}", head_dim);
+    if (kv_stride < (int64_t)n_kv_head * head_dim || (kv_stride * 2) % 16)
+        return set_error(ULLM_HIP_E_INVALID, "prefill: kv_stride must be >= n_kv_head*head_dim and 16-byte aligned");
+    if (S == 0) return ULLM_HIP_OK;
+    if (!q || !k_cache || !v_cache || !out)
+        return set_error(ULLM_HIP_E_INVALID, "prefill: null tensor pointer");
+    if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) & 15)
+        return set_error(ULLM_HIP_E_INVALID, "prefill: tensors must be 16-byte aligned");
+    const float qs = scale * kLog2e;
+    const int kv_mul = n_head / n_kv_head;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == ULLM_DT_BF16)
+        return dispatch_prefill<BF16>(head_dim, q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
+    return dispatch_prefill<F16>(head_dim, q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
+}
