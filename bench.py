@@ -1,0 +1,312 @@
+"""Benchmark of the uLLM attention path on one MI355X.
+
+Headline workload: Qwen2.5-1.5B-shaped decode
+attention -- batch 1, 12 query heads, 2 KV heads, head_dim 128, f16 KV cache
+of 4096 positions, 28 layers back to back.  One step = the attention of all
+28 layers for one decoded token, inputs resident in HBM.  The KV sets rotate
+over >= 512 MiB so the 256 MiB Infinity Cache cannot serve them.
+
+Also reported on the same line: causal prefill (configs[2], Qwen3-4B-shaped,
+S=2048 bf16) in TFLOP/s, long-context decode (configs[4], 32K bf16), the
+roofline of the dominant kernel and the CPU oracle on a bounded sample.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|long|copy]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode-attn µs/layer + HBM GB/s at 4K ctx; prefill-attn TFLOP/s (1 GPU)"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "copy"], default="all")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return ap.parse_args()
+
+
+def decode_workload(torch, A, H, Hk, D, L, n_layer, dt, min_bytes):
+    """Rotating sets of per-layer (q, K, V) plus one captured graph per set."""
+    dev = torch.device("cuda")
+    layer_bytes = 2 * L * Hk * D * torch.finfo(dt).bits // 8
+    n_sets = max(1, math.ceil(min_bytes / (layer_bytes * n_layer)))
+    g = torch.Generator(device=dev).manual_seed(1234)
+    sets = []
+    for _ in range(n_sets):
+        k = torch.randn(n_layer, L, Hk * D, generator=g, device=dev).to(dt)
+        v = torch.randn(n_layer, L, Hk * D, generator=g, device=dev).to(dt)
+        q = torch.randn(n_layer, 1, H, D, generator=g, device=dev)
+        sets.append((q, k, v))
+    lens = torch.tensor([L], dtype=torch.int32, device=dev)
+    ws = A.new_decode_workspace(1, H, Hk, D, L)
+    out = torch.empty(n_layer, 1, H, D, device=dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def step_eager(si, events=None):
+        q, k, v = sets[si]
+        for li in range(n_layer):
+            if events is not None:
+                events[li][0].record()
+            A.attn_decode(q[li], k[li], v[li], lens, L, Hk, scale=scale, out=out[li],
+                          workspace=ws)
+            if events is not None:
+                events[li][1].record()
+
+    # Warm the kernels, then capture one graph per set (no memsets inside).
+    for si in range(n_sets):
+        step_eager(si)
+    torch.cuda.synchronize()
+    graphs = []
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        for si in range(n_sets):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=cap):
+                step_eager(si)
+            graphs.append(gr)
+    torch.cuda.current_stream().wait_stream(cap)
+    torch.cuda.synchronize()
+    return dict(sets=sets, graphs=graphs, step_eager=step_eager, layer_bytes=layer_bytes,
+                n_sets=n_sets, out=out, n_layer=n_layer)
+
+
+def time_graph_steps(torch, wl, steps, warmup):
+    graphs, n = wl["graphs"], wl["n_sets"]
+    for i in range(warmup):
+        graphs[i % n].replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    t0.record()
+    for i in range(steps):
+        graphs[i % n].replay()
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    return t0.elapsed_time(t1) / steps, wall
+
+
+def time_kernel_launches(torch, wl, steps):
+    """Average kernel duration: an event pair around every launch."""
+    n_layer = wl["n_layer"]
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n_layer)] for _ in range(steps)]
+    for i in range(steps):
+        wl["step_eager"](i % wl["n_sets"], ev[i])
+    torch.cuda.synchronize()
+    d = [a.elapsed_time(b) for row in ev for (a, b) in row]
+    return sum(d) / len(d)
+
+
+def bench_decode(torch, A, args, H, Hk, D, L, n_layer, dt, label):
+    wl = decode_workload(torch, A, H, Hk, D, L, n_layer, dt, 2 * MALL_BYTES)
+    ms_step, wall = time_graph_steps(torch, wl, args.steps, args.warmup)
+    k_ms = time_kernel_launches(torch, wl, max(5, min(args.steps, 50)))
+    us_layer = ms_step * 1000.0 / n_layer
+    lb = wl["layer_bytes"]
+    return dict(label=label, ms_per_step=ms_step, us_per_layer=us_layer,
+                gbps_step=lb / (us_layer * 1e3), kernel_us=k_ms * 1000.0,
+                gbps_kernel=lb / (k_ms * 1e6), layer_bytes=lb, n_sets=wl["n_sets"],
+                wall_s=wall)
+
+
+def bench_prefill(torch, A, args, S, H, Hk, D, dt):
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(99)
+    q = torch.randn(S, H * D, generator=g, device=dev).to(dt)
+    k = torch.randn(S, Hk * D, generator=g, device=dev).to(dt)
+    v = torch.randn(S, Hk * D, generator=g, device=dev).to(dt)
+    out = torch.empty(S, H * D, device=dev)
+    run = lambda: A.attn_prefill(q, k, v, H, Hk, D, out=out)  # noqa: E731
+    for _ in range(max(3, args.warmup)):
+        run()
+    torch.cuda.synchronize()
+    n = max(10, min(args.steps, 100))
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n)]
+    for a, b in ev:
+        a.record()
+        run()
+        b.record()
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(b) for a, b in ev) / n
+    flop = 4.0 * D * H * S * (S + 1) / 2  # causal pairs only
+    return dict(ms=ms, tflops=flop / (ms * 1e-3) / 1e12, flop=flop, launches=n)
+
+
+def bench_copy(torch):
+    """Plain copy of known size: the calibration kernel for FETCH/WRITE_SIZE."""
+    n = 256 << 20
+    a = torch.ones(n // 4, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return dict(bytes_each_way=n)
+
+
+def cpu_baseline_decode(H, Hk, D, L, n_layer, budget_s=10.0):
+    """The oracle (single thread, reference schedule) on layers of the same shape."""
+    import numpy as np
+
+    from oracle import oracle as ora
+
+    rng = np.random.default_rng(7)
+    kc = rng.standard_normal((L, Hk * D), dtype=np.float32).astype(np.float16).astype(np.float32)
+    vc = rng.standard_normal((L, Hk * D), dtype=np.float32).astype(np.float16).astype(np.float32)
+    q = rng.standard_normal(H * D, dtype=np.float32)
+    scale = 1.0 / math.sqrt(D)
+    done, t0 = 0, time.perf_counter()
+    while done < n_layer * 4 and time.perf_counter() - t0 < budget_s:
+        ora.attn_decode(q, kc, vc, L - 1, H, Hk, D, scale)
+        done += 1
+    el = time.perf_counter() - t0
+    return dict(value=el / done * 1e6, unit="us/layer", cores=1, kind="port",
+                sample=f"{done} layer(s) of the cfg2 decode shape on 1 thread "
+                       f"({el:.1f} s), oracle/ref_attention.c -O2")
+
+
+def cpu_baseline_prefill(S, H, Hk, D, n_rows=12):
+    import numpy as np
+
+    from oracle import oracle as ora
+
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((S, H * D), dtype=np.float32)
+    kc = rng.standard_normal((S, Hk * D), dtype=np.float32)
+    vc = rng.standard_normal((S, Hk * D), dtype=np.float32)
+    rows = [int(r) for r in np.linspace(0, S - 1, n_rows)]
+    t0 = time.perf_counter()
+    ora.attn_prefill(q, kc, vc, S, 0, H, Hk, D, 1.0 / math.sqrt(D), rows=rows)
+    el = time.perf_counter() - t0
+    flop = sum(4.0 * D * H * (r + 1) for r in rows)
+    rate = flop / el
+    full = 4.0 * D * H * S * (S + 1) / 2
+    return dict(gflops=rate / 1e9, est_full_ms=full / rate * 1e3, rows=n_rows, seconds=el)
+
+
+def load_traffic():
+    p = os.path.join(ROOT, "profiles", "decode_cfg2_traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f)
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build targets ONE GPU; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from ullm_amd import attention as A
+
+    A.L.lib()  # fail loudly if the HIP library is missing
+    if args.only == "copy":
+        print(json.dumps(bench_copy(torch)))
+        return
+    res = {}
+    if args.only in ("all", "decode"):
+        res["cfg2"] = bench_decode(torch, A, args, 12, 2, 128, 4096, 28, torch.float16, "cfg2")
+    if args.only in ("all", "prefill"):
+        res["cfg3"] = bench_prefill(torch, A, args, 2048, 32, 8, 128, torch.bfloat16)
+    if args.only in ("all", "long"):
+        res["cfg5"] = bench_decode(torch, A, argparse.Namespace(steps=max(5, args.steps // 10),
+                                                                warmup=3),
+                                   32, 4, 128, 32768, 48, torch.bfloat16, "cfg5")
+    if args.only != "all":
+        print(json.dumps(res))
+        return
+
+    d, p, lc = res["cfg2"], res["cfg3"], res["cfg5"]
+    traffic = load_traffic()
+    line = {
+        "metric": METRIC,
+        "value": round(d["us_per_layer"], 4),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(d["ms_per_step"], 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": "cfg2 Qwen2.5-1.5B-shaped decode attention: batch 1, 12 q heads, "
+                        "2 kv heads, head_dim 128, f16 KV cache 4096, 28 layers per step "
+                        "(HIP graph per step, KV sets rotated over "
+                        f"{d['n_sets']} x 28 layers to defeat the MALL)",
+            "batch": 1, "n_head": 12, "n_kv_head": 2, "head_dim": 128, "ctx": 4096,
+            "layers": 28, "kv_dtype": "f16",
+        },
+        "decode_gbps": round(d["gbps_step"], 1),
+        "decode_kernel_us": round(d["kernel_us"], 3),
+        "decode_kernel_gbps": round(d["gbps_kernel"], 1),
+        "prefill": {"workload": "cfg3 Qwen3-4B-shaped causal prefill, S=2048, 32/8 heads, "
+                                "head_dim 128, bf16", "ms": round(p["ms"], 4),
+                    "tflops": round(p["tflops"], 2),
+                    "flop_causal": p["flop"]},
+        "long_decode": {"workload": "cfg5 Qwen3-30B-A3B-shaped decode, 32/4 heads, head_dim "
+                                    "128, bf16 KV 32768, 48 layers",
+                        "us_per_layer": round(lc["us_per_layer"], 3),
+                        "gbps": round(lc["gbps_step"], 1),
+                        "kernel_us": round(lc["kernel_us"], 3),
+                        "kernel_gbps": round(lc["gbps_kernel"], 1),
+                        "frac_hbm": round(lc["gbps_kernel"] / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(d["gbps_kernel"], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(d["gbps_kernel"] / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get("bytes_per_launch") if traffic else None,
+                     "kernel": "decode_split_kernel<F16,128,6>",
+                     "algorithmic_bytes": d["layer_bytes"]},
+        "roofline_prefill": {"bound": "mfma", "achieved": round(p["tflops"], 2),
+                             "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(p["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+                             "kernel": "prefill_kernel<BF16,128>"},
+    }
+    if not args.no_cpu:
+        cb = cpu_baseline_decode(12, 2, 128, 4096, 28)
+        cp = cpu_baseline_prefill(2048, 32, 8, 128)
+        cb["prefill_sample"] = (f"{cp['rows']} rows x 32 heads of cfg3 in {cp['seconds']:.1f} s:"
+                                f" {cp['gflops']:.2f} GFLOP/s, full prefill est. "
+                                f"{cp['est_full_ms']:.0f} ms")
+        cb["host_cpu"] = _cpu_model()
+        cb["nproc"] = os.cpu_count()
+        line["cpu_baseline"] = cb
+    print(json.dumps(line))
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    main()

@@ -85,6 +85,12 @@ inline int check_hip(hipError_t e, const char *what) {
 inline int dtype_bytes(int dt) { return dt == ULLM_DT_F32 ? 4 : 2; }
 inline bool dtype_ok(int dt) { return dt == ULLM_DT_F32 || dt == ULLM_DT_F16 || dt == ULLM_DT_BF16; }
 
+// MFMA decode path for f16/bf16 caches (decode_mfma.hip).
+size_t decode_mfma_workspace(int batch, int n_head, int n_kv_head, int D, int max_len, int window);
+int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64_t kvs,
+                int64_t ss, const int32_t *lens, int max_len, int win, int batch, int nh, int nkv,
+                int D, float qs, float *out, void *ws, size_t ws_bytes, hipStream_t st);
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 }  // namespace ullm

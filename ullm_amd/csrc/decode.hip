@@ -22,10 +22,12 @@
 //  * Softmax runs in the exp2 domain: q is pre-multiplied by scale*log2(e).
 #include "common.hpp"
 #include "wave.hpp"
+#include <cstdlib>
 
 namespace ullm {
 
 constexpr int kDecodeWaves = 8;
+constexpr int kTargetWorkgroups = 256;  // about one per CU
 
 template <class T, int D, int G>
 struct DecodeCfg {
@@ -161,15 +163,19 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
     }
 
     // Merge the waves through LDS.
+    constexpr int kMaxSplitsG = 256;               // splits * G cap (planner)
+    constexpr int R_ = (NW * 64) / (G * D / 4) > 0 ? (NW * 64) / (G * D / 4) : 1;
+    constexpr int kAccFloats = NW * G * D;
+    constexpr int kMergeFloats = 2 * kMaxSplitsG + 8 + R_ * G * D;
     __shared__ float sm_ml[NW][G][2];
-    __shared__ float sm_acc[NW][G][D];
+    __shared__ __attribute__((aligned(16))) float sm_acc[1][1][kAccFloats > kMergeFloats ? kAccFloats : kMergeFloats];
     __shared__ int sm_last;
     if (lane < LPT) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
             if (lane == 0) { sm_ml[wave][g][0] = m[g]; sm_ml[wave][g][1] = l[g]; }
 #pragma unroll
-            for (int e = 0; e < EPL; e++) sm_acc[wave][g][sub * EPL + e] = acc[g][e];
+            for (int e = 0; e < EPL; e++) sm_acc[0][0][(wave * G + g) * D + sub * EPL + e] = acc[g][e];
         }
     }
     __syncthreads();
@@ -185,7 +191,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
 #pragma unroll
         for (int w = 0; w < NW; w++) {
             const float c = exp2f(sm_ml[w][g][0] - mu);
-            num += sm_acc[w][g][d] * c;
+            num += sm_acc[0][0][(w * G + g) * D + d] * c;
             den += sm_ml[w][g][1] * c;
         }
         if (splits == 1) {
@@ -211,19 +217,54 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
     if (!sm_last) return;
     __threadfence();
 
+    // Merge all splits of this unit.  Loads are issued in parallel: m/l go
+    // to LDS first, then thread (column of 4 d, split residue r) walks its
+    // share of the splits and the R residues are summed through LDS.
     const float *mlu = ws_ml + unit * splits * G * 2;
     const float *accu = ws_acc + unit * splits * (G * D);
+    float *sw = &sm_acc[0][0][0];                 // [splits*G] weights, reused LDS
+    float *sl = sw + kMaxSplitsG;                 // [splits*G] partial sums l
+    float *sden = sl + kMaxSplitsG;               // [G] denominators
+    for (int i = tid; i < splits * G; i += NW * 64) {
+        sw[i] = mlu[2 * i];
+        sl[i] = mlu[2 * i + 1];
+    }
+    __syncthreads();
+    if (tid < G) {
+        float mx = -INFINITY;
+        for (int sp = 0; sp < splits; sp++) mx = fmaxf(mx, sw[sp * G + tid]);
+        sm_ml[0][tid][0] = (mx == -INFINITY) ? 0.f : mx;
+    }
+    __syncthreads();
+    for (int i = tid; i < splits * G; i += NW * 64) sw[i] = exp2f(sw[i] - sm_ml[0][i % G][0]);
+    __syncthreads();
+    if (tid < G) {
+        float den = 0.f;
+        for (int sp = 0; sp < splits; sp++) den += sl[sp * G + tid] * sw[sp * G + tid];
+        sden[tid] = den;
+    }
+    constexpr int NCOL = G * D / 4;
+    constexpr int R = (NW * 64) / NCOL > 0 ? (NW * 64) / NCOL : 1;
+    float *sred = sden + 8;                       // [R][G*D] partial sums
+    if (tid < NCOL * R) {
+        const int col = tid % NCOL, r = tid / NCOL;
+        const int g = (col * 4) / D;
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+        for (int sp = r; sp < splits; sp += R) {
+            const f32x4 v = *(const f32x4 *)(accu + (int64_t)sp * (G * D) + col * 4);
+            const float w = sw[sp * G + g];
+            a[0] += v[0] * w; a[1] += v[1] * w; a[2] += v[2] * w; a[3] += v[3] * w;
+        }
+        *(f32x4 *)(sred + r * (G * D) + col * 4) = a;
+    }
+    __syncthreads();
     for (int idx = tid; idx < G * D; idx += NW * 64) {
         const int g = idx / D, d = idx % D;
-        float mx = -INFINITY;
-        for (int sp = 0; sp < splits; sp++) mx = fmaxf(mx, mlu[(sp * G + g) * 2]);
-        const float mu = (mx == -INFINITY) ? 0.f : mx;
-        float num = 0.f, den = 0.f;
-        for (int sp = 0; sp < splits; sp++) {
-            const float c = exp2f(mlu[(sp * G + g) * 2] - mu);
-            num += accu[sp * (G * D) + idx] * c;
-            den += mlu[(sp * G + g) * 2 + 1] * c;
-        }
+        float num = 0.f;
+#pragma unroll
+        for (int r = 0; r < R; r++) num += sred[r * (G * D) + idx];
+        const float den = sden[g];
         out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
     }
     if (tid == 0) counters[unit] = 0u;  // leave the counter ready for the next call
@@ -259,15 +300,24 @@ static DecodePlan plan_decode(int batch, int n_head, int n_kv_head, int D, int d
     p.nlg = kDecodeWaves * (64 / lpt);
     const int visible = (window > 0 && max_len > window) ? window : max_len;
     const int units = batch * p.n_groups;
-    const int target_wg = 512, max_splits = 128;
-    int splits = (target_wg + units - 1) / units;
-    if (splits > max_splits) splits = max_splits;
+    // tile = keys one workgroup covers per iteration (every lane group busy).
+    const int epl = 16 / dtype_bytes(dtype);
+    const int tt = (p.G * epl <= 48) ? 8 : 4;
+    const int tile = p.nlg * tt;
+    int splits = (visible + tile - 1) / tile;             // >= one full tile per split
+    const int want = (kTargetWorkgroups + units - 1) / units;
+    if (splits > want) splits = want;
+    const int merge_cap = 256 / p.G;                       // merge reads <= 256 partial rows
+    if (splits > merge_cap) splits = merge_cap;
+    if (const char *e = getenv("ULLM_HIP_DECODE_SPLITS")) {  // tuning override
+        const int f = atoi(e);
+        if (f >= 1) splits = f < merge_cap ? f : merge_cap;
+    }
+    if (splits < 1) splits = 1;
     int chunk = (visible + splits - 1) / splits;
     chunk = ((chunk + p.nlg - 1) / p.nlg) * p.nlg;
-    if (chunk < p.nlg) chunk = p.nlg;
     p.chunk = chunk;
     p.splits = (visible + chunk - 1) / chunk;
-    if (p.splits < 1) p.splits = 1;
     const size_t ctr = ((size_t)units * 4 + 255) / 256 * 256;
     const size_t ml = ((size_t)units * p.splits * p.G * 2 * 4 + 255) / 256 * 256;
     const size_t ac = (size_t)units * p.splits * p.G * D * 4;
@@ -341,12 +391,9 @@ extern "C" size_t ullm_hip_decode_workspace_bytes(int batch, int n_head, int n_k
     if (batch < 1 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || max_len < 1) return 0;
     // The f32 cache has the most lanes per key and thus the smallest chunks:
     // size for the largest plan over the three dtypes.
-    size_t best = 0;
-    for (int dt = 0; dt < 3; dt++) {
-        DecodePlan p = plan_decode(batch, n_head, n_kv_head, head_dim, dt, max_len, window);
-        if (p.bytes > best) best = p.bytes;
-    }
-    return best;
+    size_t best = plan_decode(batch, n_head, n_kv_head, head_dim, ULLM_DT_F32, max_len, window).bytes;
+    const size_t m = decode_mfma_workspace(batch, n_head, n_kv_head, head_dim, max_len, window);
+    return m > best ? m : best;
 }
 
 extern "C" int ullm_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache,
@@ -363,17 +410,17 @@ extern "C" int ullm_hip_attn_decode(const float *q, const void *k_cache, const v
         return set_error(ULLM_HIP_E_INVALID, "decode: q/k_cache/v_cache must be 16-byte aligned");
     if (batch > 1 && (seq_stride * dtype_bytes(kv_dtype)) % 16)
         return set_error(ULLM_HIP_E_INVALID, "decode: seq_stride must be 16-byte aligned");
+    const float qscale = scale * kLog2e;
+    hipStream_t st = (hipStream_t)stream;
+    if (kv_dtype != ULLM_DT_F32)
+        return decode_mfma(kv_dtype, q, k_cache, v_cache, kv_stride, seq_stride, seq_lens, max_len,
+                           window, batch, n_head, n_kv_head, head_dim, qscale, out, workspace,
+                           workspace_bytes, st);
     DecodePlan p = plan_decode(batch, n_head, n_kv_head, head_dim, kv_dtype, max_len, window);
     if (p.bytes > 0 && (!workspace || workspace_bytes < p.bytes))
         return set_error(ULLM_HIP_E_WORKSPACE, "decode: workspace of %zu bytes needed, %zu given",
                          p.bytes, workspace_bytes);
-    const float qscale = scale * kLog2e;
     const int kv_mul = n_head / n_kv_head;
-    hipStream_t st = (hipStream_t)stream;
-    char *ws = (char *)workspace;
-    switch (kv_dtype) {
-        case ULLM_DT_F32: return dispatch_d<F32>(head_dim, p, q, k_cache, v_cache, kv_stride, seq_stride, seq_lens, window, batch, n_head, kv_mul, qscale, out, ws, st);
-        case ULLM_DT_F16: return dispatch_d<F16>(head_dim, p, q, k_cache, v_cache, kv_stride, seq_stride, seq_lens, window, batch, n_head, kv_mul, qscale, out, ws, st);
-        default: return dispatch_d<BF16>(head_dim, p, q, k_cache, v_cache, kv_stride, seq_stride, seq_lens, window, batch, n_head, kv_mul, qscale, out, ws, st);
-    }
+    return dispatch_d<F32>(head_dim, p, q, k_cache, v_cache, kv_stride, seq_stride, seq_lens,
+                           window, batch, n_head, kv_mul, qscale, out, (char *)workspace, st);
 }
