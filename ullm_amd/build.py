@@ -52,6 +52,13 @@ def build(verbose: bool = True) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
+    # Fail here, not on the GPU box, if a kernel stub or symbol went missing.
+    import ctypes
+
+    try:
+        ctypes.CDLL(os.path.abspath(tmp))
+    except OSError as e:
+        raise RuntimeError(f"built library does not load: {e}") from None
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources", file=sys.stderr)

@@ -45,6 +45,18 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// Two f32 -> packed 16-bit pair (low = a), round-to-nearest-even in hardware
+// (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
+}
+
 // Widen one 16-byte chunk (4 f32 or 8 half-precision values) to f32.
 template <class T> struct Chunk;
 template <> struct Chunk<F32> {

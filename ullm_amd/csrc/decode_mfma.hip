@@ -40,10 +40,18 @@ constexpr int kMW = 4;          // waves per workgroup
 constexpr int kTok = 32;        // keys per wave iteration (two 16-key tiles)
 constexpr int kMaxUnitHeads = 16;
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, gfx9 data format
-constexpr int kMfmaTargetWG = 512;
+constexpr int kMfmaTargetWG = 256;  // one 4-wave workgroup per CU (LDS-bound)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Pointer known to be wave-uniform, kept in SGPRs.
+__device__ __forceinline__ void *uniform_ptr(const void *p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (void *)(((uint64_t)hi << 32) | lo);
+}
 
 // Compiler-only ordering point for wave-private LDS traffic.
 __device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
@@ -58,16 +66,25 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4 &a, const u32x4 &b, const f3
                                                       __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-// f32 -> 16-bit storage of T (RNE) and back.
+// Pair of f32 -> packed 16-bit pair of T (hardware RNE), and back.
 template <class T>
-__device__ __forceinline__ uint32_t to16(float f) {
-    if constexpr (__is_same(T, BF16)) return f32_to_bf16_bits(f);
-    else return f32_to_f16_bits(f);
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (__is_same(T, BF16)) return pack_bf16x2(a, b);
+    else return pack_f16x2(a, b);
 }
 template <class T>
-__device__ __forceinline__ float from16(uint32_t h) {
-    if constexpr (__is_same(T, BF16)) return __uint_as_float(h << 16);
-    else return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+__device__ __forceinline__ void unpack2(uint32_t w, float &a, float &b) {
+    if constexpr (__is_same(T, BF16)) { a = bf16_lo(w); b = bf16_hi(w); }
+    else { a = f16_lo(w); b = f16_hi(w); }
+}
+// x = hi + lo with hi, lo in T: ~2x the mantissa bits of T.
+// Returns {hi, lo} packed pairs.
+template <class T>
+__device__ __forceinline__ u32x2 split2(float x0, float x1) {
+    const uint32_t hi = pack2<T>(x0, x1);
+    float h0, h1;
+    unpack2<T>(hi, h0, h1);
+    return u32x2{hi, pack2<T>(x0 - h0, x1 - h1)};
 }
 
 template <class T, int D>
@@ -83,12 +100,25 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     constexpr bool SPLITP = __is_same(T, BF16);
 
     const int split = blockIdx.x, unit = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int n16 = lane & 15, kg = lane >> 4;
     const int head0 = unit * gt, kvh = head0 / kv_mul;
     const bool head_ok = n16 < gt;
 
-    const int len = seq_lens[b];
+    // Raw q loads go out first (vmcnt retires in order, so q must precede
+    // the K/V stream to be waited for on its own).
+    f32x4 qa[NS][2];
+    {
+        const float *qp = q + ((int64_t)b * n_head + head0 + (head_ok ? n16 : 0)) * D;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            qa[s][0] = *(const f32x4 *)(qp + (s * 4 + kg) * 8);
+            qa[s][1] = *(const f32x4 *)(qp + (s * 4 + kg) * 8 + 4);
+        }
+    }
+
+    const int len = __builtin_amdgcn_readfirstlane(seq_lens[b]);
     const int start = (window > 0 && len > window) ? len - window : 0;
     const int c0 = start + split * chunk;
     const int c1 = min(c0 + chunk, len);
@@ -96,30 +126,7 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     __shared__ __attribute__((aligned(16))) uint16_t vt_all[kMW][kTok * VP];
     uint16_t *vt = vt_all[wave];
 
-    // Q^T operand, hi/lo split: step s, lane (head n16, chunk c = s*4 + kg).
-    // All q loads are issued before any is used (one round trip).
-    u32x4 qh[NS], ql[NS];
-    {
-        const float *qp = q + ((int64_t)b * n_head + head0 + (head_ok ? n16 : 0)) * D;
-        f32x4 qa[NS][2];
-#pragma unroll
-        for (int s = 0; s < NS; s++) {
-            qa[s][0] = *(const f32x4 *)(qp + (s * 4 + kg) * 8);
-            qa[s][1] = *(const f32x4 *)(qp + (s * 4 + kg) * 8 + 4);
-        }
-#pragma unroll
-        for (int s = 0; s < NS; s++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float x0 = head_ok ? qa[s][j >> 1][(2 * j) & 3] * qscale : 0.f;
-                const float x1 = head_ok ? qa[s][j >> 1][(2 * j + 1) & 3] * qscale : 0.f;
-                const uint32_t h0 = to16<T>(x0), h1 = to16<T>(x1);
-                const uint32_t l0 = to16<T>(x0 - from16<T>(h0)), l1 = to16<T>(x1 - from16<T>(h1));
-                qh[s][j] = h0 | (h1 << 16);
-                ql[s][j] = l0 | (l1 << 16);
-            }
-    }
-
+    u32x4 qh[NS], ql[NS];  // Q^T operand (filled once the first block is in flight)
     f32x4 oacc[NDT];
 #pragma unroll
     for (int i = 0; i < NDT; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -131,8 +138,10 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     const char *kb0 = kc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
     const char *vb0 = vc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
     const int range = c1 > 0 ? (c1 - 1) * rb + D * 2 : 0;
-    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void *)kb0, 0, range, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void *)vb0, 0, range, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kb0), 0, range, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vb0), 0, range, kRsrcWord3);
 
     // V is staged row-major: lane l loads 16-byte chunk (l % CPR) of key
     // (l / CPR) + KPI*i of the block and writes it unchanged to the wave's LDS
@@ -153,7 +162,7 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     const int voffb = vrow0 * rb + vcol * 16;
     // Issue the loads of the block starting at key tb (nontemporal).
     auto issue = [&](Tile &T_, int tb) {
-        const int so = tb * rb;
+        const int so = __builtin_amdgcn_readfirstlane(tb * rb);
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -184,12 +193,17 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
             *(u32x4 *)(vt + (vrow0 + i * KPI) * VP + vcol * 8) = T_.v[i];
         // online softmax: lane = head n16, keys kg*4+i (tile 0) and 16+kg*4+i
         float sv[8];
-        const bool full = tb + kTok <= c1;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                sv[t * 4 + i] = (full || tb + t * 16 + kg * 4 + i < c1) ? sacc[t][i] : -INFINITY;
+            for (int i = 0; i < 4; i++) sv[t * 4 + i] = sacc[t][i];
+        if (tb + kTok > c1) {  // partial block (wave-uniform branch)
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (tb + t * 16 + kg * 4 + i >= c1) sv[t * 4 + i] = -INFINITY;
+        }
         float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                          fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
         mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
@@ -209,12 +223,12 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
         u32x4 ph, pl;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const uint32_t h0 = to16<T>(p[2 * j]), h1 = to16<T>(p[2 * j + 1]);
-            ph[j] = h0 | (h1 << 16);
             if constexpr (SPLITP) {
-                const uint32_t l0 = to16<T>(p[2 * j] - from16<T>(h0));
-                const uint32_t l1 = to16<T>(p[2 * j + 1] - from16<T>(h1));
-                pl[j] = l0 | (l1 << 16);
+                const u32x2 hl = split2<T>(p[2 * j], p[2 * j + 1]);
+                ph[j] = hl[0];
+                pl[j] = hl[1];
+            } else {
+                ph[j] = pack2<T>(p[2 * j], p[2 * j + 1]);
             }
         }
         // O^T += V^T . P^T.  The LDS tile is private to this wave and a wave's
@@ -241,10 +255,24 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     // stage and streams one block at a time).
     constexpr int STEP = kMW * kTok;
     int tb = c0 + wave * kTok;
+    Tile A_;
+    issue(A_, tb);  // first block in flight while q is prepared (past c1: zeros)
+
+    // Q^T operand, hi/lo split: step s, lane (head n16, chunk c = s*4 + kg).
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float x0 = head_ok ? qa[s][j >> 1][(2 * j) & 3] * qscale : 0.f;
+            const float x1 = head_ok ? qa[s][j >> 1][(2 * j + 1) & 3] * qscale : 0.f;
+            const u32x2 hl = split2<T>(x0, x1);
+            qh[s][j] = hl[0];
+            ql[s][j] = hl[1];
+        }
+
     if constexpr (D <= 128) {
-        Tile A_, B_;
+        Tile B_;
         if (tb < c1) {
-            issue(A_, tb);
             for (;;) {
                 const int tn = tb + STEP;
                 issue(B_, tn);
@@ -259,9 +287,8 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
         }
     } else {
         for (; tb < c1; tb += STEP) {
-            Tile A_;
-            issue(A_, tb);
             consume(A_, tb);
+            if (tb + STEP < c1) issue(A_, tb + STEP);
         }
     }
 
@@ -312,14 +339,297 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
 
 namespace ullm {
 
-constexpr int kMaxSplits = 128;
-constexpr int kMergeLoads = 32;  // per-thread partial loads kept in flight
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14; expcnt and
+// lgkmcnt left at their maxima).
+constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-// Combines the split partials of one (sequence, head): all loads are issued
-// at once -- m/l of every split into LDS, and thread (column of 4 d, split
-// residue r) holds its splits' partial rows in registers -- then the
-// log-sum-exp weights are applied and the residues summed through LDS.
-template <int D>
+// LDS-staged variant for head_dim <= 128: K and V tiles go global -> LDS by
+// buffer_load ... lds (no staging registers), each instruction covering whole
+// contiguous head rows of 4 (D=128) or 8 (D=64) keys.  A row of the tile is
+// D*2 bytes in 16-byte slots; slot p of row r holds chunk p ^ (r % SLOTS), an
+// XOR swizzle applied by permuting the global chunk each lane fetches, so the
+// MFMA-operand reads below hit distinct banks.  K operands come from
+// ds_read_b128, V^T operands from the transposing ds_read_b64_tr_b16.  Each
+// wave owns two stages (double buffering); the wait for a stage leaves the
+// other stage's transfers in flight.
+typedef __attribute__((address_space(3))) void lds_void;
+
+// LDS reads of DMA-filled tiles, issued as inline asm: the compiler would
+// otherwise treat every LDS read as possibly aliasing in-flight LDS DMA and
+// wait for all of it (vmcnt(0)), serialising the two-stage pipeline.  The
+// caller waits with lds_wait() (tied to the destination registers) before use.
+// One 16-byte-per-lane buffer load straight into LDS (lane i -> dst + 16 i),
+// nontemporal; out-of-range offsets read zero.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char *dst, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, voff, soff, 0, 2);
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+__device__ __forceinline__ u32x4 lds_read_b128(uint32_t a) {
+    u32x4 r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+__device__ __forceinline__ u32x2 lds_read_tr16_b64(uint32_t a) {
+    u32x2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x4 (&r)[N]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" : "+v"(r[i]));
+}
+
+template <class T, int D>
+__global__ __launch_bounds__(kMW * 64, 1) void decode_dma_kernel(
+    const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
+    int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
+    int n_head, int kv_mul, int gt, int n_units, int chunk, int splits, float qscale,
+    float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc) {
+    constexpr int NS = D / 32;          // QK k-steps (32 d each)
+    constexpr int NDT = D / 16;         // 16-wide d tiles of O^T
+    constexpr int RB = D * 2;           // bytes per key row of one head
+    constexpr int SLOTS = D / 8;        // 16-byte slots per row
+    constexpr int RPI = 1024 / RB;      // rows written by one DMA instruction
+    constexpr int NI = kTok / RPI;      // DMA instructions per K (or V) tile
+    constexpr int TILE = kTok * RB;     // bytes of one K (or V) tile
+    constexpr int STAGE = 2 * TILE;     // K tile then V tile
+    constexpr bool SPLITP = __is_same(T, BF16);
+    static_assert(D == 64 || D == 128, "DMA decode path covers head_dim 64 and 128");
+
+    const int split = blockIdx.x, unit = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n16 = lane & 15, kg = lane >> 4;
+    const int head0 = unit * gt, kvh = head0 / kv_mul;
+    const bool head_ok = n16 < gt;
+
+    // One array per stage: the stage a read targets is then a distinct
+    // object from the stage the DMA is filling, which keeps the compiler from
+    // draining all DMA (vmcnt(0)) before every LDS read.
+    __shared__ __attribute__((aligned(1024))) char lds0[kMW * STAGE];
+    __shared__ __attribute__((aligned(1024))) char lds1[kMW * STAGE];
+    char *const wb0 = lds0 + wave * STAGE;
+    char *const wb1 = lds1 + wave * STAGE;
+
+    const int len = __builtin_amdgcn_readfirstlane(seq_lens[b]);
+    const int start = (window > 0 && len > window) ? len - window : 0;
+    const int c0 = start + split * chunk;
+    const int c1 = min(c0 + chunk, len);
+
+    const int rb = (int)(kv_stride * 2);
+    const char *kb0 = kc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
+    const char *vb0 = vc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
+    const int range = c1 > 0 ? (c1 - 1) * rb + D * 2 : 0;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kb0), 0, range, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vb0), 0, range, kRsrcWord3);
+
+    // DMA lane map: instruction i writes rows i*RPI + lane/SLOTS, slot lane%SLOTS.
+    const int drow = lane / SLOTS, dslot = lane % SLOTS;
+    int dofs[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int r = i * RPI + drow;
+        dofs[i] = r * rb + ((dslot ^ (r & (SLOTS - 1))) * 16);
+    }
+    auto issue = [&](char *kt, int tb) {
+        const int so = __builtin_amdgcn_readfirstlane(tb * rb);
+        char *vt = kt + TILE;
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            dma16(krs, kt + i * 1024, dofs[i], so);
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            dma16(vrs, vt + i * 1024, dofs[i], so);
+    };
+
+    constexpr int STEP = kMW * kTok;
+    const int tb0 = c0 + wave * kTok;
+    issue(wb0, tb0);
+    issue(wb1, tb0 + STEP);
+
+    // q is loaded after the first two DMA stages are queued; vmcnt retires in
+    // order, so waiting for q also waits for data the first block needs.
+    f32x4 qa[NS][2];
+    {
+        const float *qp = q + ((int64_t)b * n_head + head0 + (head_ok ? n16 : 0)) * D;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            qa[s][0] = *(const f32x4 *)(qp + (s * 4 + kg) * 8);
+            qa[s][1] = *(const f32x4 *)(qp + (s * 4 + kg) * 8 + 4);
+        }
+    }
+
+
+    u32x4 qh[NS], ql[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float x0 = head_ok ? qa[s][j >> 1][(2 * j) & 3] * qscale : 0.f;
+            const float x1 = head_ok ? qa[s][j >> 1][(2 * j + 1) & 3] * qscale : 0.f;
+            const u32x2 hl = split2<T>(x0, x1);
+            qh[s][j] = hl[0];
+            ql[s][j] = hl[1];
+        }
+
+    f32x4 oacc[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_part = 0.f;
+
+    auto consume = [&](const char *kt, int tb) {
+        const char *vt = kt + TILE;
+        // S^T = K . Q^T: lane (key t*16 + n16, chunk s*4 + kg)
+        const uint32_t kbase = lds_addr(kt);
+        u32x4 ka[2 * NS];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int r = t * 16 + n16;
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+                ka[t * NS + s] = lds_read_b128(kbase + r * RB + (((s * 4 + kg) ^ (r & (SLOTS - 1))) * 16));
+        }
+        lds_wait(ka);
+        f32x4 sacc[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                sacc[t] = mfma16<T>(ka[t * NS + s], qh[s], sacc[t]);
+                sacc[t] = mfma16<T>(ka[t * NS + s], ql[s], sacc[t]);
+            }
+        }
+        float sv[8];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) sv[t * 4 + i] = sacc[t][i];
+        if (tb + kTok > c1) {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (tb + t * 16 + kg * 4 + i >= c1) sv[t * 4 + i] = -INFINITY;
+        }
+        float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                         fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float m_new = fmaxf(m_run, mt);
+        const float mu = m_new == -INFINITY ? 0.f : m_new;
+        if (__any(m_new != m_run)) {
+            const float corr = __builtin_amdgcn_exp2f(m_run - mu);
+            l_part *= corr;
+#pragma unroll
+            for (int i = 0; i < NDT; i++) oacc[i] *= corr;
+        }
+        m_run = m_new;
+        float p[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) { p[i] = __builtin_amdgcn_exp2f(sv[i] - mu); l_part += p[i]; }
+        u32x4 ph, pl;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if constexpr (SPLITP) {
+                const u32x2 hl = split2<T>(p[2 * j], p[2 * j + 1]);
+                ph[j] = hl[0];
+                pl[j] = hl[1];
+            } else {
+                ph[j] = pack2<T>(p[2 * j], p[2 * j + 1]);
+            }
+        }
+        // O^T += V^T . P^T; lane n16 of key group kg reads V rows kg*4 + n16/4
+        // (+16), elements dt*16 + 4*(n16 % 4) .. +3, transposed by the read.
+        const int vr0 = kg * 4 + (n16 >> 2);
+        const uint32_t vbase = lds_addr(vt);
+        u32x4 va[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            const int ch = dt * 2 + ((n16 & 3) >> 1);
+            const int bo = 8 * (n16 & 1);
+            const u32x2 l2 = lds_read_tr16_b64(vbase + vr0 * RB + ((ch ^ (vr0 & (SLOTS - 1))) * 16) + bo);
+            const u32x2 h2 = lds_read_tr16_b64(vbase + (vr0 + 16) * RB +
+                                               ((ch ^ ((vr0 + 16) & (SLOTS - 1))) * 16) + bo);
+            va[dt] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+        }
+        lds_wait(va);
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            oacc[dt] = mfma16<T>(va[dt], ph, oacc[dt]);
+            if constexpr (SPLITP) oacc[dt] = mfma16<T>(va[dt], pl, oacc[dt]);
+        }
+    };
+    // Unrolled by the two stages; each stage is refilled once its LDS reads
+    // have retired (lgkmcnt(0)), two blocks ahead.
+    constexpr int kLgkm0 = vm_wait(63) & ~(15 << 8);
+    for (int tb = tb0; tb < c1; tb += 2 * STEP) {
+        __builtin_amdgcn_s_waitcnt(vm_wait(2 * NI));  // stage 0 landed, stage 1 in flight
+        consume(wb0, tb);
+        __builtin_amdgcn_s_waitcnt(kLgkm0);
+        issue(wb0, tb + 2 * STEP);
+        if (tb + STEP >= c1) break;
+        __builtin_amdgcn_s_waitcnt(vm_wait(2 * NI));
+        consume(wb1, tb + STEP);
+        __builtin_amdgcn_s_waitcnt(kLgkm0);
+        issue(wb1, tb + 3 * STEP);
+    }
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));  // drain DMA before the LDS is reused
+
+    l_part += __shfl_xor(l_part, 16, 64);
+    l_part += __shfl_xor(l_part, 32, 64);
+    __syncthreads();
+    float *sm = (float *)lds0;  // kMW*16*(D+2) floats fit in one stage array
+    float *sm_m = sm, *sm_l = sm + kMW * 16, *sm_o = sm + 2 * kMW * 16;
+    if (kg == 0) { sm_m[wave * 16 + n16] = m_run; sm_l[wave * 16 + n16] = l_part; }
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) sm_o[(wave * 16 + n16) * D + dt * 16 + kg * 4 + i] = oacc[dt][i];
+    __syncthreads();
+    const int64_t u = (int64_t)b * n_units + unit;
+    const int GD = gt * D;
+    for (int idx = tid; idx < GD; idx += kMW * 64) {
+        const int g = idx / D, d = idx % D;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kMW; w++) mx = fmaxf(mx, sm_m[w * 16 + g]);
+        const float mu = mx == -INFINITY ? 0.f : mx;
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (int w = 0; w < kMW; w++) {
+            const float c = exp2f(sm_m[w * 16 + g] - mu);
+            num += sm_o[(w * 16 + g) * D + d] * c;
+            den += sm_l[w * 16 + g] * c;
+        }
+        if (splits == 1) {
+            out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
+        } else {
+            ws_acc[(u * splits + split) * GD + idx] = num;
+            if (d == 0) {
+                ws_ml[((u * splits + split) * gt + g) * 2] = mx;
+                ws_ml[((u * splits + split) * gt + g) * 2 + 1] = den;
+            }
+        }
+    }
+}
+
+constexpr int kMaxSplits = 128;
+
+// Combines the split partials of one (sequence, head) in one round trip:
+// every load (the split rows of this thread's column group, then this
+// thread's split m/l) is issued branch-free (indices clamped, weights of
+// clamped duplicates zeroed) before any is consumed; then the log-sum-exp
+// weights are applied and the R split residues summed through LDS.
+// NL = partial rows per thread, ceil(splits / R).
+template <int D, int NL>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float *__restrict__ ws_ml,
                                                            const float *__restrict__ ws_acc,
                                                            int splits, int gt, int n_units,
@@ -331,26 +641,25 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float *__restri
     const int GD = gt * D;
     __shared__ float sm_m[kMaxSplits], sm_l[kMaxSplits];
     __shared__ f32x4 red[R][NC];
-    for (int sp = tid; sp < splits; sp += 256) {
-        sm_m[sp] = ws_ml[((u * splits + sp) * gt + g) * 2];
-        sm_l[sp] = ws_ml[((u * splits + sp) * gt + g) * 2 + 1];
-    }
-    f32x4 v[kMergeLoads];
+    const float *accp = ws_acc + u * splits * GD + g * D + col * 4;
+    f32x4 v[NL];
 #pragma unroll
-    for (int i = 0; i < kMergeLoads; i++) {
-        const int sp = r + i * R;
-        v[i] = sp < splits ? *(const f32x4 *)(ws_acc + (u * splits + sp) * GD + g * D + col * 4)
-                           : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int i = 0; i < NL; i++)
+        v[i] = *(const f32x4 *)(accp + (int64_t)min(r + i * R, splits - 1) * GD);
+    const int spm = min(tid, splits - 1);
+    const float mv = ws_ml[((u * splits + spm) * gt + g) * 2];
+    const float lv = ws_ml[((u * splits + spm) * gt + g) * 2 + 1];
+    if (tid < splits) { sm_m[tid] = mv; sm_l[tid] = lv; }
     __syncthreads();
     float mx = -INFINITY;
     for (int sp = 0; sp < splits; sp++) mx = fmaxf(mx, sm_m[sp]);
     const float mu = mx == -INFINITY ? 0.f : mx;
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < kMergeLoads; i++) {
+    for (int i = 0; i < NL; i++) {
         const int sp = r + i * R;
-        if (sp < splits) a += v[i] * exp2f(sm_m[sp] - mu);
+        const float w = sp < splits ? exp2f(sm_m[min(sp, splits - 1)] - mu) : 0.f;
+        a += v[i] * w;
     }
     red[r][col] = a;
     __syncthreads();
@@ -411,18 +720,44 @@ size_t decode_mfma_workspace(int batch, int n_head, int n_kv_head, int D, int ma
     return plan_mfma(batch, n_head, n_kv_head, D, max_len, window).bytes;
 }
 
+// head_dim <= 128 streams through LDS DMA; 256 keeps register staging.
+template <class T, int D, bool DMA = (D <= 128)>
+struct MainLaunch {
+    template <class... A>
+    static void run(dim3 g, hipStream_t st, A... a) {
+        hipLaunchKernelGGL((decode_dma_kernel<T, D>), g, dim3(kMW * 64), 0, st, a...);
+    }
+};
+template <class T, int D>
+struct MainLaunch<T, D, false> {
+    template <class... A>
+    static void run(dim3 g, hipStream_t st, A... a) {
+        hipLaunchKernelGGL((decode_mfma_kernel<T, D>), g, dim3(kMW * 64), 0, st, a...);
+    }
+};
+
 template <class T, int D>
 static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const void *vc,
                         int64_t kvs, int64_t ss, const int32_t *lens, int win, int batch, int nh,
                         int kv_mul, float qs, float *out, char *ws, hipStream_t st) {
-    hipLaunchKernelGGL((decode_mfma_kernel<T, D>), dim3(p.splits, p.n_units, batch),
-                       dim3(kMW * 64), 0, st, q, (const char *)kc, (const char *)vc, kvs, ss,
-                       lens, win, nh, kv_mul, p.gt, p.n_units, p.chunk, p.splits, qs, out,
-                       (float *)(ws + p.off_ml), (float *)(ws + p.off_acc));
-    if (p.splits > 1)
-        hipLaunchKernelGGL((decode_merge_kernel<D>), dim3(p.gt, p.n_units, batch), dim3(256), 0,
-                           st, (const float *)(ws + p.off_ml), (const float *)(ws + p.off_acc),
-                           p.splits, p.gt, p.n_units, nh, out);
+    MainLaunch<T, D>::run(dim3(p.splits, p.n_units, batch), st, q, (const char *)kc,
+                          (const char *)vc, kvs, ss, lens, win, nh, kv_mul, p.gt, p.n_units,
+                          p.chunk, p.splits, qs, out, (float *)(ws + p.off_ml),
+                          (float *)(ws + p.off_acc));
+    if (p.splits > 1) {
+        constexpr int R = 256 / (D / 4);
+        const int nl = (p.splits + R - 1) / R;
+        const dim3 g(p.gt, p.n_units, batch);
+        const float *ml = (const float *)(ws + p.off_ml), *ac = (const float *)(ws + p.off_acc);
+#define ULLM_MERGE(NL) hipLaunchKernelGGL((decode_merge_kernel<D, NL>), g, dim3(256), 0, st, ml, \
+                                          ac, p.splits, p.gt, p.n_units, nh, out)
+        if (nl <= 2) ULLM_MERGE(2);
+        else if (nl <= 4) ULLM_MERGE(4);
+        else if (nl <= 8) ULLM_MERGE(8);
+        else if (nl <= 16) ULLM_MERGE(16);
+        else ULLM_MERGE(32);
+#undef ULLM_MERGE
+    }
 }
 
 int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64_t kvs,
