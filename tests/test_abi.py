@@ -1,0 +1,97 @@
+"""C ABI of libullm_hip.so without a GPU: loading, exported symbols, the host
+RoPE table, and argument validation (all return before touching the device)."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import oracle as ora
+from ullm_amd import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    src = open(os.path.join(ROOT, "include", "ullm_hip.h")).read()
+    return sorted(set(re.findall(r"\b(ullm_hip_\w+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_function():
+    lib = L.lib()
+    names = header_functions()
+    assert len(names) >= 7
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in L.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_version():
+    assert L.lib().ullm_hip_version().decode().startswith("ullm-hip ")
+
+
+@pytest.mark.parametrize("neox", [True, False])
+def test_rope_table_reproduces_reference_rope_exactly(neox):
+    """The host table gives the CPU reference's rotation bit for bit
+    (same f32 angle, same libm)."""
+    hd, n_pos = 128, 4096
+    cs = np.empty((n_pos, hd // 2, 2), np.float32)
+    L.check(L.lib().ullm_hip_rope_table(C.c_void_p(cs.ctypes.data), n_pos, hd, 1e6))
+    rng = np.random.default_rng(0)
+    for pos in (0, 1, 77, 4095):
+        v = rng.standard_normal(hd).astype(np.float32)
+        want = ora.rope(v, 1, hd, hd, pos, 1e6, neox)
+        c, s = cs[pos, :, 0], cs[pos, :, 1]
+        if neox:
+            a, b = v[: hd // 2], v[hd // 2:]
+            got = np.concatenate([a * c - b * s, a * s + b * c])
+        else:
+            a, b = v[0::2], v[1::2]
+            got = np.empty_like(v)
+            got[0::2], got[1::2] = a * c - b * s, a * s + b * c
+        np.testing.assert_array_equal(got, want)
+
+
+def _decode(**kw):
+    args = dict(q=None, k=None, v=None, dt=L.DT_F16, kvs=256, ss=0, lens=None, max_len=100,
+                win=0, b=1, h=12, hk=2, d=128, scale=0.1, out=None, ws=None, wsb=0, st=None)
+    args.update(kw)
+    a = args
+    return L.lib().ullm_hip_attn_decode(a["q"], a["k"], a["v"], a["dt"], a["kvs"], a["ss"],
+                                         a["lens"], a["max_len"], a["win"], a["b"], a["h"],
+                                         a["hk"], a["d"], a["scale"], a["out"], a["ws"],
+                                         a["wsb"], a["st"])
+
+
+def test_decode_argument_validation():
+    assert _decode(d=96) == L.E_UNSUPPORTED
+    assert _decode(dt=7) == L.E_UNSUPPORTED
+    assert _decode(h=12, hk=5) == L.E_INVALID
+    assert _decode(max_len=0) == L.E_INVALID
+    assert _decode(kvs=100) == L.E_INVALID
+    assert _decode() == L.E_INVALID  # null tensors
+    assert b"null" in L.lib().ullm_hip_last_error()
+
+
+def test_prefill_and_append_validation():
+    lib = L.lib()
+    assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_F32, 256, 16, 0, 0, 8, 2, 128, 0.1,
+                                     None, None) == L.E_UNSUPPORTED
+    assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_BF16, 256, 16, 0, 0, 8, 3, 128,
+                                     0.1, None, None) == L.E_INVALID
+    assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_BF16, 256, 0, 0, 0, 8, 2, 128, 0.1,
+                                     None, None) == L.OK  # S == 0 is a no-op
+    rc = lib.ullm_hip_qkv_append(None, None, None, None, None, None, None, None, 1e-6, None, 10,
+                                 1, 128, 4, 8, 8, 2, 128, None, L.DT_F32, None, None, L.DT_F16,
+                                 256, None)
+    assert rc == L.E_INVALID  # rope table shorter than start_pos + rows
+    assert lib.ullm_hip_rope_table(None, 10, 128, 1e4) == L.E_INVALID
+
+
+def test_workspace_size_planning():
+    ws = L.lib().ullm_hip_decode_workspace_bytes
+    assert ws(1, 12, 2, 128, 4096, 0) > 0
+    assert ws(1, 12, 2, 128, 64, 0) == 0  # one split: no partials
+    assert ws(1, 32, 4, 128, 32768, 0) >= ws(1, 32, 4, 128, 4096, 0)
+    assert ws(1, 12, 5, 128, 4096, 0) == 0  # invalid shape
