@@ -29,63 +29,15 @@
 //    counter) combines the partials and writes `out`.
 #include <cstdlib>
 #include "common.hpp"
+#include "mfma_util.hpp"
 #include "wave.hpp"
 
 namespace ullm {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-
 constexpr int kMW = 4;          // waves per workgroup
 constexpr int kTok = 32;        // keys per wave iteration (two 16-key tiles)
 constexpr int kMaxUnitHeads = 16;
-constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, gfx9 data format
 constexpr int kMfmaTargetWG = 256;  // one 4-wave workgroup per CU (LDS-bound)
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// Pointer known to be wave-uniform, kept in SGPRs.
-__device__ __forceinline__ void *uniform_ptr(const void *p) {
-    const uint64_t v = (uint64_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return (void *)(((uint64_t)hi << 32) | lo);
-}
-
-// Compiler-only ordering point for wave-private LDS traffic.
-__device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
-
-template <class T>
-__device__ __forceinline__ f32x4 mfma16(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
-    if constexpr (__is_same(T, BF16))
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-    else
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
-                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
-}
-
-// Pair of f32 -> packed 16-bit pair of T (hardware RNE), and back.
-template <class T>
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-    if constexpr (__is_same(T, BF16)) return pack_bf16x2(a, b);
-    else return pack_f16x2(a, b);
-}
-template <class T>
-__device__ __forceinline__ void unpack2(uint32_t w, float &a, float &b) {
-    if constexpr (__is_same(T, BF16)) { a = bf16_lo(w); b = bf16_hi(w); }
-    else { a = f16_lo(w); b = f16_hi(w); }
-}
-// x = hi + lo with hi, lo in T: ~2x the mantissa bits of T.
-// Returns {hi, lo} packed pairs.
-template <class T>
-__device__ __forceinline__ u32x2 split2(float x0, float x1) {
-    const uint32_t hi = pack2<T>(x0, x1);
-    float h0, h1;
-    unpack2<T>(hi, h0, h1);
-    return u32x2{hi, pack2<T>(x0 - h0, x1 - h1)};
-}
 
 template <class T, int D>
 __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel(
@@ -168,11 +120,11 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
 #pragma unroll
             for (int s = 0; s < NS; s++)
                 T_.k[t][s] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koffb[t] + s * 64, so, 2));
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koffb[t] + s * 64 + so, 0, 2));
 #pragma unroll
         for (int i = 0; i < VL; i++)
             T_.v[i] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voffb + i * KPI * rb, so, 2));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voffb + i * KPI * rb + so, 0, 2));
     };
     // Consume a loaded block.
     auto consume = [&](Tile &T_, int tb) {
@@ -339,11 +291,6 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
 
 namespace ullm {
 
-// s_waitcnt immediate that waits until at most n vector-memory operations
-// are outstanding (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14; expcnt and
-// lgkmcnt left at their maxima).
-constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
 // LDS-staged variant for head_dim <= 128: K and V tiles go global -> LDS by
 // buffer_load ... lds (no staging registers), each instruction covering whole
 // contiguous head rows of 4 (D=128) or 8 (D=64) keys.  A row of the tile is
@@ -353,36 +300,6 @@ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (
 // ds_read_b128, V^T operands from the transposing ds_read_b64_tr_b16.  Each
 // wave owns two stages (double buffering); the wait for a stage leaves the
 // other stage's transfers in flight.
-typedef __attribute__((address_space(3))) void lds_void;
-
-// LDS reads of DMA-filled tiles, issued as inline asm: the compiler would
-// otherwise treat every LDS read as possibly aliasing in-flight LDS DMA and
-// wait for all of it (vmcnt(0)), serialising the two-stage pipeline.  The
-// caller waits with lds_wait() (tied to the destination registers) before use.
-// One 16-byte-per-lane buffer load straight into LDS (lane i -> dst + 16 i),
-// nontemporal; out-of-range offsets read zero.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char *dst, int voff, int soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, voff, soff, 0, 2);
-}
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
-}
-__device__ __forceinline__ u32x4 lds_read_b128(uint32_t a) {
-    u32x4 r;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
-    return r;
-}
-__device__ __forceinline__ u32x2 lds_read_tr16_b64(uint32_t a) {
-    u32x2 r;
-    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
-    return r;
-}
-template <int N>
-__device__ __forceinline__ void lds_wait(u32x4 (&r)[N]) {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < N; i++) asm volatile("" : "+v"(r[i]));
-}
 
 template <class T, int D>
 __global__ __launch_bounds__(kMW * 64, 1) void decode_dma_kernel(
@@ -443,10 +360,10 @@ __global__ __launch_bounds__(kMW * 64, 1) void decode_dma_kernel(
         char *vt = kt + TILE;
 #pragma unroll
         for (int i = 0; i < NI; i++)
-            dma16(krs, kt + i * 1024, dofs[i], so);
+            dma16(krs, kt + i * 1024, dofs[i] + so, 0);
 #pragma unroll
         for (int i = 0; i < NI; i++)
-            dma16(vrs, vt + i * 1024, dofs[i], so);
+            dma16(vrs, vt + i * 1024, dofs[i] + so, 0);
     };
 
     constexpr int STEP = kMW * kTok;

@@ -1,0 +1,129 @@
+// Device helpers shared by the MFMA attention kernels: 16-bit packing, MFMA
+// wrappers, buffer resources, LDS DMA and LDS reads that bypass the
+// compiler's LDS-DMA alias tracking.
+#pragma once
+#include "common.hpp"
+
+namespace ullm {
+
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource word 3 (gfx9 data format)
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Pointer known to be wave-uniform, kept in SGPRs.
+__device__ __forceinline__ void *uniform_ptr(const void *p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (void *)(((uint64_t)hi << 32) | lo);
+}
+
+// Compiler-only ordering point for wave-private LDS traffic.
+__device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
+
+template <class T>
+__device__ __forceinline__ f32x4 mfma16(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
+    if constexpr (__is_same(T, BF16))
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// Pair of f32 -> packed 16-bit pair of T (hardware RNE), and back.
+template <class T>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (__is_same(T, BF16)) return pack_bf16x2(a, b);
+    else return pack_f16x2(a, b);
+}
+template <class T>
+__device__ __forceinline__ void unpack2(uint32_t w, float &a, float &b) {
+    if constexpr (__is_same(T, BF16)) { a = bf16_lo(w); b = bf16_hi(w); }
+    else { a = f16_lo(w); b = f16_hi(w); }
+}
+// x = hi + lo with hi, lo in T: ~2x the mantissa bits of T.
+// Returns {hi, lo} packed pairs.
+template <class T>
+__device__ __forceinline__ u32x2 split2(float x0, float x1) {
+    const uint32_t hi = pack2<T>(x0, x1);
+    float h0, h1;
+    unpack2<T>(hi, h0, h1);
+    return u32x2{hi, pack2<T>(x0 - h0, x1 - h1)};
+}
+
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14; expcnt and
+// lgkmcnt left at their maxima).
+constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// LDS reads of DMA-filled tiles, issued as inline asm: the compiler would
+// otherwise treat every LDS read as possibly aliasing in-flight LDS DMA and
+// wait for all of it (vmcnt(0)), serialising the two-stage pipeline.  The
+// caller waits with lds_wait() (tied to the destination registers) before use.
+// One 16-byte-per-lane buffer load straight into LDS (lane i -> dst + 16 i),
+// nontemporal.  Offsets past the resource's range read zero; the range check
+// covers the per-lane offset, so callers put every variable part there and
+// keep the scalar offset at 0.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char *dst, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, voff, soff, 0, 2);
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+__device__ __forceinline__ u32x4 lds_read_b128(uint32_t a) {
+    u32x4 r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+__device__ __forceinline__ void lds_write_b128(uint32_t a, const u32x4 &v) {
+    asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+__device__ __forceinline__ u32x2 lds_read_tr16_b64(uint32_t a) {
+    u32x2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x4 (&r)[N]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" : "+v"(r[i]));
+}
+
+}  // namespace ullm
+
+namespace ullm {
+
+template <class T>
+__device__ __forceinline__ f32x16 mfma32(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
+    if constexpr (__is_same(T, BF16))
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// Waits for this wave's outstanding LDS reads and ties the results to the
+// wait so the compiler cannot use them earlier.
+__device__ __forceinline__ void lds_wait_any() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void tie(u32x4 &r) { asm volatile("" : "+v"(r)); }
+__device__ __forceinline__ void tie(u32x2 &r) { asm volatile("" : "+v"(r)); }
+
+// Workgroup barrier without a memory fence (LDS DMA visibility is ensured by
+// each wave's own vmcnt wait before it).
+__device__ __forceinline__ void wg_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+}  // namespace ullm

@@ -27,6 +27,7 @@
 //    row block first; blocks are dealt to the 8 XCDs so that all query heads
 //    of one kv head share one XCD's L2 (workgroup i runs on XCD i % 8).
 #include "common.hpp"
+#include "mfma_util.hpp"
 #include "wave.hpp"
 
 namespace ullm {
@@ -244,16 +245,325 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void prefill_kernel(
         }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill v2: K/V tiles shared by 8 waves through a 3-stage LDS ring filled by
+// buffer_load ... lds (whole contiguous head rows per instruction, 16-byte
+// slots XOR-swizzled by row); K operands via ds_read_b128, V^T operands via
+// the transposing ds_read_b64_tr_b16 from the row-major V tile.
+//
+// Work: a "unit" is HW query heads of one kv head (HW = 4, 2 or 1 heads,
+// dividing the GQA group) and a "group" is RW = 4/HW consecutive 32-row
+// blocks, so 4 waves cover one group.  A workgroup = 8 waves = two groups:
+// without a window they are g and NG-1-g, so every workgroup carries the same
+// causal work (no tail of short workgroups); with a window they are adjacent.
+// Each wave owns 32 query rows of one head.
+template <int D>
+struct PF2 {
+    static constexpr int NW = 8;
+    static constexpr int BN = D <= 128 ? 64 : 32;   // keys per tile
+    static constexpr int RB = D * 2;                // LDS bytes per key row
+    static constexpr int SLOTS = D / 8;             // 16-byte slots per row
+    static constexpr int RPI = 1024 / RB;           // rows per DMA instruction
+    static constexpr int NI = BN / RPI;             // DMA instructions per K (or V) tile
+    static constexpr int NIW = NI / NW;             // ... per wave
+    static constexpr int TILE = BN * RB;
+    static constexpr int STAGE = 2 * TILE;
+    static constexpr int NSTG = 3;
+    static constexpr int NKT = BN / 32;             // 32-key MFMA tiles per tile
+    static constexpr int NKS = D / 16;              // QK k-steps
+    static constexpr int NDT = D / 32;              // output d tiles
+    static_assert(NIW >= 1 && NI % NW == 0, "DMA split");
+};
+
+template <class T, int D>
+__global__ __launch_bounds__(512) void prefill2_kernel(
+    const uint16_t *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
+    int64_t kv_stride, int S, int start_pos, int window, int n_head, int kv_mul, int hw,
+    int rw, int n_units, int ng, int np, int paired, float qscale, float *__restrict__ out) {
+    using C = PF2<D>;
+    constexpr int BN = C::BN, RB = C::RB, SLOTS = C::SLOTS, RPI = C::RPI, NIW = C::NIW;
+    constexpr int TILE = C::TILE, STAGE = C::STAGE, NKT = C::NKT, NKS = C::NKS, NDT = C::NDT;
+    constexpr bool CVTV = __is_same(T, BF16);  // bf16 V is widened to f16 in LDS
+    __shared__ __attribute__((aligned(1024))) char lds[C::NSTG * STAGE];
+
+    // ---- work assignment (XCD-aware: one unit's workgroups share an L2) ----
+    const int total = n_units * np;
+    const int per_xcd = (total + 7) / 8;
+    const int t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (t >= total) return;
+    const int unit = t / np, pair = t % np;
+    const int n_sub = kv_mul / hw;
+    const int kvh = unit / n_sub;
+    const int head0 = kvh * kv_mul + (unit % n_sub) * hw;
+    const int gA = paired ? pair : 2 * pair;
+    const int gB = paired ? ng - 1 - pair : 2 * pair + 1;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int half = wave >> 2, slot = wave & 3;
+    const int kv_len = start_pos + S;
+
+    // Key range of one wave (uniform): rows of block (group, slot).
+    auto wave_rows = [&](int w, int &row0, int &lo, int &hi) {
+        const int g = (w >> 2) ? gB : gA;
+        const bool dup = (w >> 2) && gB == gA;
+        row0 = (g * rw + (w & 3) / hw) * 32;
+        if (g >= ng || dup || row0 >= S) { lo = 1 << 30; hi = -1; return; }
+        hi = start_pos + min(row0 + 32, S);
+        lo = window > 0 ? max(0, start_pos + row0 + 1 - window) : 0;
+    };
+    int lo = 1 << 30, hi = -1;
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+        int r0, l0, h0;
+        wave_rows(w, r0, l0, h0);
+        lo = min(lo, l0);
+        hi = max(hi, h0);
+    }
+    int row0, wlo, whi;
+    wave_rows(wave, row0, wlo, whi);
+    const int head = head0 + slot % hw;
+    const bool active = whi > 0;
+
+    // ---- buffer resources (out-of-range reads return zero) ----
+    const int rbg = (int)(kv_stride * 2);
+    const int range = (kv_len - 1) * rbg + D * 2;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
+
+    // DMA lane map: this wave writes instructions wave*NIW + i of each tile.
+    int dofs[NIW];
+#pragma unroll
+    for (int i = 0; i < NIW; i++) {
+        const int r = (wave * NIW + i) * RPI + lane / SLOTS;
+        dofs[i] = r * rbg + (((lane % SLOTS) ^ (r & (SLOTS - 1))) * 16);
+    }
+    const int kt0 = hi > 0 ? (max(lo, 0) / BN) : 0;
+    const int nt = hi > 0 ? (hi + BN - 1) / BN - kt0 : 0;
+    auto issue = [&](int tt) {
+        const int so = __builtin_amdgcn_readfirstlane((kt0 + tt) * BN * rbg);
+        char *st = lds + (tt % C::NSTG) * STAGE;
+#pragma unroll
+        for (int i = 0; i < NIW; i++) {
+            dma16(krs, st + (wave * NIW + i) * 1024, dofs[i] + so, 0);
+            dma16(vrs, st + TILE + (wave * NIW + i) * 1024, dofs[i] + so, 0);
+        }
+    };
+
+    // ---- Q rows of this wave: B operand, d = s*16 + (lane/32)*8 + j ----
+    const int c32 = lane & 31, h2 = lane >> 5;
+    const int64_t q_dim = (int64_t)n_head * D;
+    u32x4 qreg[NKS];
+    {
+        const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+            uniform_ptr(q), 0, (int)((int64_t)S * q_dim * 2), kRsrcWord3);
+        const int qo = (int)(((int64_t)(row0 + c32) * q_dim + (int64_t)head * D + h2 * 8) * 2);
+#pragma unroll
+        for (int s = 0; s < NKS; s++)
+            qreg[s] = active ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                   qrs, qo + s * 32, 0, 0))
+                             : u32x4{0, 0, 0, 0};
+    }
+    const int pos_row = start_pos + row0 + c32;
+
+    f32x16 oacc[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
+    float m_run = -INFINITY, l_part = 0.f;
+
+    // bf16 -> f16 of one V tile in LDS: each thread widens 16-byte chunks
+    // (exact for |v| < 65504: bf16's 8-bit mantissa fits f16's 11 bits).
+    auto widen_v = [&](int tt) {
+        if constexpr (CVTV) {
+            const uint32_t vb = lds_addr(lds + (tt % C::NSTG) * STAGE + TILE);
+            constexpr int CH = TILE / 16 / (C::NW * 64);  // chunks per thread
+            u32x4 w[CH];
+#pragma unroll
+            for (int c = 0; c < CH; c++) w[c] = lds_read_b128(vb + (c * C::NW * 64 + tid) * 16);
+            lds_wait_any();
+#pragma unroll
+            for (int c = 0; c < CH; c++) {
+                tie(w[c]);
+                u32x4 o;
+#pragma unroll
+                for (int j = 0; j < 4; j++) o[j] = pack_f16x2(bf16_lo(w[c][j]), bf16_hi(w[c][j]));
+                lds_write_b128(vb + (c * C::NW * 64 + tid) * 16, o);
+            }
+        }
+    };
+    // Ring: tiles tt+1 and tt+2 are in flight while tile tt computes; the V of
+    // tile tt+1 is widened during iteration tt, before the barrier that
+    // publishes it.
+    if (nt > 0) {
+        issue(0);
+        issue(1);
+        __builtin_amdgcn_s_waitcnt(vm_wait(2 * NIW));  // own DMA of tile 0 landed
+        wg_barrier();
+        widen_v(0);  // published by the first barrier of the loop
+    }
+    for (int tt = 0; tt < nt; tt++) {
+        // own DMA of tile tt+1 landed and own LDS writes (widened V) retired
+        __builtin_amdgcn_s_waitcnt(vm_wait(0) & ~(15 << 8));
+        wg_barrier();  // tile tt+1 landed everywhere; V(tt) widened; tile tt-1 consumed
+        issue(tt + 2);
+        widen_v(tt + 1);
+        const int kb = (kt0 + tt) * BN;
+        if (!active || kb >= whi || kb + BN <= wlo) continue;
+        const char *kt_ = lds + (tt % C::NSTG) * STAGE, *vt_ = kt_ + TILE;
+        const uint32_t kbase = lds_addr(kt_), vbase = lds_addr(vt_);
+
+        // ---- S^T = K . Q^T ----
+        f32x16 sacc[NKT];
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++) {
+            const int r = kt * 32 + c32;
+            u32x4 ka[NKS];
+#pragma unroll
+            for (int s = 0; s < NKS; s++)
+                ka[s] = lds_read_b128(kbase + r * RB + (((s * 2 + h2) ^ (r & (SLOTS - 1))) * 16));
+            lds_wait_any();
+#pragma unroll
+            for (int s = 0; s < NKS; s++) tie(ka[s]);
+            sacc[kt] = f32x16{};
+#pragma unroll
+            for (int s = 0; s < NKS; s++) sacc[kt] = mfma32<T>(ka[s], qreg[s], sacc[kt]);
+        }
+
+        // ---- online softmax (lane = query row c32; keys (i/4)*8 + h2*4 + i%4) ----
+        // Scores stay unscaled; qscale > 0 so the max commutes with scaling,
+        // and scaling is folded into the exp2 argument (one FMA per score).
+        const bool need_mask = (kb + BN - 1 > start_pos + row0) ||
+                               (window > 0 && kb <= start_pos + row0 + 31 - window);
+        if (need_mask) {
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int key = kb + kt * 32 + (i >> 2) * 8 + h2 * 4 + (i & 3);
+                    const bool dead = key > pos_row || (window > 0 && key <= pos_row - window);
+                    sacc[kt][i] = dead ? -INFINITY : sacc[kt][i];
+                }
+        }
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) mloc = fmaxf(mloc, sacc[kt][i]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * qscale;
+        const float m_new = fmaxf(m_run, mloc);
+        const float mu = m_new == -INFINITY ? 0.f : m_new;
+        if (__any(m_new != m_run)) {
+            const float corr = __builtin_amdgcn_exp2f(m_run - mu);
+            l_part *= corr;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) oacc[dt] *= corr;
+        }
+        m_run = m_new;
+        u32x4 ph[NKT][2];
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][ks * 8 + 2 * jj], qscale, -mu));
+                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][ks * 8 + 2 * jj + 1], qscale, -mu));
+                    l_part += p0 + p1;
+                    ph[kt][ks][jj] = pack_f16x2(p0, p1);
+                }
+
+        // ---- O^T += V^T . P^T: two transposing reads per 16-key k-step ----
+        const int g16 = lane >> 4, i16 = lane & 15, hh = g16 >> 1;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            const int e0 = dt * 32 + (g16 & 1) * 16 + 4 * (i16 & 3);
+            const int chq = e0 >> 3, boff = (e0 & 7) * 2;
+            u32x4 va[NKT][2];
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) {
+                    const int R0 = kt * 32 + ks * 16 + hh * 4 + (i16 >> 2);
+                    const int R1 = R0 + 8;
+                    const u32x2 a0 = lds_read_tr16_b64(vbase + R0 * RB + ((chq ^ (R0 & (SLOTS - 1))) * 16) + boff);
+                    const u32x2 a1 = lds_read_tr16_b64(vbase + R1 * RB + ((chq ^ (R1 & (SLOTS - 1))) * 16) + boff);
+                    va[kt][ks] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+                }
+            lds_wait_any();
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) {
+                    tie(va[kt][ks]);
+                    oacc[dt] = mfma32<F16>(va[kt][ks], ph[kt][ks], oacc[dt]);
+                }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));  // no DMA may outlive the workgroup
+
+    if (!active) return;
+    const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    const int qrow = row0 + c32;
+    if (qrow >= S) return;
+    float *op = out + (int64_t)qrow * q_dim + (int64_t)head * D + h2 * 4;
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            f32x4 v = {oacc[dt][g * 4] * inv, oacc[dt][g * 4 + 1] * inv, oacc[dt][g * 4 + 2] * inv,
+                       oacc[dt][g * 4 + 3] * inv};
+            *(f32x4 *)(op + dt * 32 + g * 8) = v;
+        }
+}
+
+// head_dim 256 keeps the register-staged kernel (the LDS-ring variant needs
+// more than the 256 registers two waves per SIMD allow).
+template <class T, int D, bool V2 = (D <= 128)>
+struct PrefillLaunch {
+    static void run(const void *q, const void *kc, const void *vc, int64_t kvs, int S, int sp,
+                    int win, int nh, int kv_mul, float qs, float *out, hipStream_t st) {
+        const int nqb = (S + PrefillCfg<D>::BM - 1) / PrefillCfg<D>::BM;
+        const int total = nh * nqb;
+        const int per_xcd = (total + 7) / 8;
+        hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(per_xcd * 8), dim3(256), 0, st,
+                           (const uint16_t *)q, (const uint16_t *)kc, (const uint16_t *)vc, kvs,
+                           S, sp, win, nh, kv_mul, qs, out);
+    }
+};
+template <class T, int D>
+struct PrefillLaunch<T, D, true> {
+    static void run(const void *q, const void *kc, const void *vc, int64_t kvs, int S, int sp,
+                    int win, int nh, int kv_mul, float qs, float *out, hipStream_t st);
+};
+
+template <class T, int D>
+void PrefillLaunch<T, D, true>::run(const void *q, const void *kc, const void *vc, int64_t kvs,
+                                    int S, int sp, int win, int nh, int kv_mul, float qs,
+                                    float *out, hipStream_t st) {
+    // Units of HW heads (HW | kv_mul, at most 4) x groups of RW = 4/HW 32-row blocks.
+    const int hw = kv_mul % 4 == 0 ? 4 : (kv_mul % 2 == 0 ? 2 : 1);
+    const int rw = 4 / hw;
+    const int n_units = (nh / kv_mul) * (kv_mul / hw);
+    const int ng = (S + 32 * rw - 1) / (32 * rw);
+    const int np = (ng + 1) / 2;
+    // Without an effective window the causal work of group g grows with g, so
+    // a workgroup takes g and ng-1-g; with a window it takes 2g and 2g+1.
+    const int paired = !(win > 0 && win < sp + S);
+    const int total = n_units * np;
+    const int per_xcd = (total + 7) / 8;
+    hipLaunchKernelGGL((prefill2_kernel<T, D>), dim3(per_xcd * 8), dim3(512), 0, st,
+                       (const uint16_t *)q, (const char *)kc, (const char *)vc, kvs, S, sp, win,
+                       nh, kv_mul, hw, rw, n_units, ng, np, paired, qs, out);
+}
+
 template <class T, int D>
 static int launch_prefill(const void *q, const void *kc, const void *vc, int64_t kvs, int S,
                           int sp, int win, int nh, int kv_mul, float qs, float *out,
                           hipStream_t st) {
-    const int nqb = (S + PrefillCfg<D>::BM - 1) / PrefillCfg<D>::BM;
-    const int total = nh * nqb;
-    const int per_xcd = (total + 7) / 8;
-    hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(per_xcd * 8), dim3(256), 0, st,
-                       (const uint16_t *)q, (const uint16_t *)kc, (const uint16_t *)vc, kvs, S, sp,
-                       win, nh, kv_mul, qs, out);
+    PrefillLaunch<T, D>::run(q, kc, vc, kvs, S, sp, win, nh, kv_mul, qs, out, st);
     return check_hip(hipGetLastError(), "prefill launch");
 }
 
