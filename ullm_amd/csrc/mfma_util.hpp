@@ -22,6 +22,17 @@ __device__ __forceinline__ void *uniform_ptr(const void *p) {
     return (void *)(((uint64_t)hi << 32) | lo);
 }
 
+// Compile-time loop: f(Int<0>{}) ... f(Int<N-1>{}).
+template <int V>
+struct Int { static constexpr int value = V; };
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(Int<I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
 // Compiler-only ordering point for wave-private LDS traffic.
 __device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
 
@@ -89,6 +100,22 @@ __device__ __forceinline__ void lds_write_b128(uint32_t a, const u32x4 &v) {
 __device__ __forceinline__ u32x2 lds_read_tr16_b64(uint32_t a) {
     u32x2 r;
     asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+// Same reads with a compile-time byte offset in the instruction's immediate
+// field (0..65535), so per-lane addresses can be computed once.
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_read_b128_at(uint32_t a) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    u32x4 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+    return r;
+}
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_tr16_b64_at(uint32_t a) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    u32x2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
     return r;
 }
 template <int N>

@@ -519,6 +519,339 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
         }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill v4 (head_dim <= 128, GQA groups of 4k heads, no binding window):
+// split-K inside the workgroup so that both waves of every SIMD compute at
+// every step.
+//
+// A workgroup owns 4 heads of one kv head and the causal pair of 32-row
+// blocks A = g, B = NG-1-g.  The key tiles stream in the rotated order
+// 0..TB-1, 0..TA-1 (A on tiles [0, TA), B on [TA, TB) then [0, TA): the online
+// softmax is order-free), two stream positions per step: set 0 (waves 0-3)
+// takes the even positions and set 1 (waves 4-7) the odd ones, each wave
+// keeping its own (m, l, O) for the same 32 query rows of one head.  When a
+// block is done, set 1 hands its partial over -- O/l into the output rows,
+// (m, l) through LDS -- and set 0 merges at the next step.  Every workgroup
+// streams TA+TB tiles, a constant for the causal pair, and no SIMD runs a
+// lone wave.
+//
+// LDS: K tiles of the 4 ring stages at [0, 4 TILE), V tiles at
+// [4 TILE, 8 TILE).  A wave of set s only reads stages s and s+2, so every
+// per-lane LDS address is fixed at start and the stage, key-row and k-step
+// parts go into the instructions' immediate offsets.  Each wave widens (bf16
+// -> f16) exactly the V bytes its own DMA wrote, so one barrier per step
+// orders DMA, widening and reads.
+//
+// The running max is raised only when a row's tile max exceeds it by more
+// than 2^8 (in the exp2 domain): P = exp2(s - m) then stays <= 256, exact in
+// f16's range, and the O/l rescale runs a handful of times per block instead
+// of on every new maximum.
+template <class T, int D>
+__global__ __launch_bounds__(512) void prefill4_kernel(
+    const uint16_t *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
+    int64_t kv_stride, int S, int start_pos, int n_head, int kv_mul, int ng, int np,
+    float qscale, float *__restrict__ out) {
+    using C = PF2<D>;
+    constexpr int BN = C::BN, RB = C::RB, SLOTS = C::SLOTS, RPI = C::RPI, NIW = C::NIW;
+    constexpr int TILE = C::TILE, NKT = C::NKT, NKS = C::NKS, NDT = C::NDT;
+    constexpr int NSTG = 4, VREG = NSTG * TILE;
+    constexpr bool CVTV = __is_same(T, BF16);
+    constexpr float kLazy = 8.0f;  // log2 headroom before the max is raised
+    static_assert(D <= 128 && BN == 64, "v4 tiling");
+    static_assert(2 * TILE + (NKT * 32) * RB <= 65535, "immediate offsets");
+    // 16-byte slot swizzle of key row r.  A 256-byte row (D = 128) spans all
+    // 64 banks, so the four rows one 16-lane transpose read touches must land
+    // on different slot pairs: XOR with 2r, not r.  128-byte rows (D = 64)
+    // alternate bank halves and use r itself.
+    auto swz = [](int r) { return D == 128 ? (r << 1) & (SLOTS - 1) : r & (SLOTS - 1); };
+    __shared__ __attribute__((aligned(1024))) char lds[2 * VREG];
+    __shared__ float hand_ml[2][4][32][2];
+
+    const int n_units = (n_head / kv_mul) * (kv_mul / 4);
+    const int total = n_units * np;
+    const int per_xcd = (total + 7) / 8;
+    const int tsk = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (tsk >= total) return;
+    const int unit = tsk / np, pair = tsk % np;
+    const int kvh = unit / (kv_mul / 4);
+    const int head0 = kvh * kv_mul + (unit % (kv_mul / 4)) * 4;
+    const int gA = pair, gB = ng - 1 - pair != pair ? ng - 1 - pair : -1;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int set = wave >> 2, slot = wave & 3;
+    const int c32 = lane & 31, h2 = lane >> 5;
+    const int kv_len = start_pos + S;
+    const int64_t q_dim = (int64_t)n_head * D;
+    const int head = head0 + slot;
+
+    const int rowA = gA * 32, rowB = gB >= 0 ? gB * 32 : S;
+    auto tiles_hi = [&](int row) {
+        return row < S ? (start_pos + min(row + 32, S) + BN - 1) / BN : 0;
+    };
+    const int TA = tiles_hi(rowA), TB = tiles_hi(rowB);
+    const int TB1 = max(TB, TA);
+    const int P = TB1 + (TB > 0 ? TA : 0);
+    auto stream_tile = [&](int p) { return p < TB1 ? p : p - TB1; };
+    auto task_blk = [&](int p) {  // 0 = A, 1 = B, -1 = idle
+        if (p >= P) return -1;
+        const int t = stream_tile(p);
+        if (p < TB1) return t < TA ? 0 : (t < TB ? 1 : -1);
+        return t < TA ? 1 : -1;
+    };
+
+    // ---- K/V DMA (each wave loads NIW 1 KiB chunks of every K and V tile) ----
+    const int rbg = (int)(kv_stride * 2);
+    const int range = (kv_len - 1) * rbg + D * 2;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
+    int dofs[NIW];
+#pragma unroll
+    for (int i = 0; i < NIW; i++) {
+        const int r = (wave * NIW + i) * RPI + lane / SLOTS;
+        dofs[i] = r * rbg + (((lane % SLOTS) ^ swz(r)) * 16);
+    }
+    auto issue = [&](int p) {
+        const int t = p < P ? stream_tile(p) : (kv_len + BN) / BN;  // past P: zeros
+        const int so = t * BN * rbg;
+        char *st = lds + (p % NSTG) * TILE;
+#pragma unroll
+        for (int i = 0; i < NIW; i++) {
+            dma16(krs, st + (wave * NIW + i) * 1024, dofs[i] + so, 0);
+            dma16(vrs, st + VREG + (wave * NIW + i) * 1024, dofs[i] + so, 0);
+        }
+    };
+    auto widen_own = [&](int p) {
+        if constexpr (CVTV) {
+            const uint32_t vb = lds_addr(lds + VREG + (p % NSTG) * TILE) + wave * NIW * 1024 + lane * 16;
+            u32x4 w[NIW];
+#pragma unroll
+            for (int i = 0; i < NIW; i++) w[i] = lds_read_b128(vb + i * 1024);
+            lds_wait_any();
+#pragma unroll
+            for (int i = 0; i < NIW; i++) {
+                tie(w[i]);
+                u32x4 o;
+#pragma unroll
+                for (int j = 0; j < 4; j++) o[j] = pack_f16x2(bf16_lo(w[i][j]), bf16_hi(w[i][j]));
+                lds_write_b128(vb + i * 1024, o);
+            }
+        }
+    };
+
+    // ---- fixed per-lane LDS read addresses (stage `set`, key row 0) ----
+    const uint32_t lds0 = lds_addr(lds);
+    uint32_t ka_addr[NKS];
+#pragma unroll
+    for (int s = 0; s < NKS; s++)
+        ka_addr[s] = lds0 + set * TILE + c32 * RB + (((s * 2 + h2) ^ swz(c32)) * 16);
+    const int g16 = lane >> 4, i16 = lane & 15;
+    uint32_t va_addr[NDT][2];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int e0 = dt * 32 + (g16 & 1) * 16 + 4 * (i16 & 3);
+            const int chq = e0 >> 3, boff = (e0 & 7) * 2;
+            const int R = (g16 >> 1) * 4 + (i16 >> 2) + h * 8;
+            va_addr[dt][h] = lds0 + VREG + set * TILE + R * RB + ((chq ^ swz(R)) * 16) + boff;
+        }
+
+    // ---- Q of the block being computed (reloaded once, at the A -> B switch) ----
+    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(q), 0, (int)((int64_t)S * q_dim * 2), kRsrcWord3);
+    u32x4 qv[NKS];
+    auto load_q = [&](int row) {
+        const int o = (int)((min(row + c32, S) * q_dim + (int64_t)head * D + h2 * 8) * 2);
+#pragma unroll
+        for (int s = 0; s < NKS; s++)
+            qv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qrs, o + s * 32, 0, 0));
+    };
+
+    f32x16 oacc[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
+    float m_run = -INFINITY, l_part = 0.f;
+
+    auto compute = [&](auto par, int p, int blk) {
+        constexpr int SOFF = decltype(par)::value * 2 * TILE;  // stage s or s+2
+        const int row = blk ? rowB : rowA;
+        const int kb = stream_tile(p) * BN;
+        f32x16 sacc[NKT];
+        static_for<0, NKT>([&](auto ktc) {
+            constexpr int kt = decltype(ktc)::value;
+            u32x4 ka[NKS];
+            static_for<0, NKS>([&](auto sc) {
+                constexpr int s = decltype(sc)::value;
+                ka[s] = lds_read_b128_at<SOFF + kt * 32 * RB>(ka_addr[s]);
+            });
+            lds_wait_any();
+            sacc[kt] = f32x16{};
+#pragma unroll
+            for (int s = 0; s < NKS; s++) {
+                tie(ka[s]);
+                sacc[kt] = mfma32<T>(ka[s], qv[s], sacc[kt]);
+            }
+        });
+        const int pos_row = start_pos + row + c32;
+        if (kb + BN - 1 > start_pos + row) {  // tile reaches past the block's first row
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int key = kb + kt * 32 + (i >> 2) * 8 + h2 * 4 + (i & 3);
+                    sacc[kt][i] = key > pos_row ? -INFINITY : sacc[kt][i];
+                }
+        }
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) mloc = fmaxf(mloc, sacc[kt][i]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * qscale;
+        if (__any(mloc > m_run + kLazy)) {
+            const float m_new = fmaxf(m_run, mloc);
+            const float corr = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+            l_part *= corr;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) oacc[dt] *= corr;
+            m_run = m_new;
+        }
+        const float mu = m_run == -INFINITY ? 0.f : m_run;
+        u32x4 ph[NKT][2];
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][ks * 8 + 2 * jj], qscale, -mu));
+                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][ks * 8 + 2 * jj + 1], qscale, -mu));
+                    l_part += p0 + p1;
+                    ph[kt][ks][jj] = pack_f16x2(p0, p1);
+                }
+        static_for<0, NDT>([&](auto dtc) {
+            constexpr int dt = decltype(dtc)::value;
+            u32x4 va[NKT][2];
+            static_for<0, NKT>([&](auto ktc) {
+                constexpr int kt = decltype(ktc)::value;
+                static_for<0, 2>([&](auto ksc) {
+                    constexpr int ks = decltype(ksc)::value;
+                    constexpr int off = SOFF + (kt * 32 + ks * 16) * RB;
+                    const u32x2 a0 = lds_read_tr16_b64_at<off>(va_addr[dt][0]);
+                    const u32x2 a1 = lds_read_tr16_b64_at<off>(va_addr[dt][1]);
+                    va[kt][ks] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+                });
+            });
+            lds_wait_any();
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) {
+                    tie(va[kt][ks]);
+                    oacc[dt] = mfma32<F16>(va[kt][ks], ph[kt][ks], oacc[dt]);
+                }
+        });
+    };
+
+    auto reset = [&]() {
+#pragma unroll
+        for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
+        m_run = -INFINITY;
+        l_part = 0.f;
+    };
+    // Set 1 hands its partial of block `b` to set 0: O/l into the output rows
+    // (f32), (m, l) into LDS.
+    auto hand_over = [&](int b) {
+        const int row = b ? rowB : rowA;
+        const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+        const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+        const int qrow = row + c32;
+        if (h2 == 0) { hand_ml[b][slot][c32][0] = m_run; hand_ml[b][slot][c32][1] = l_tot; }
+        if (qrow < S) {
+            float *op = out + (int64_t)qrow * q_dim + (int64_t)head * D + h2 * 4;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    *(f32x4 *)(op + dt * 32 + g * 8) =
+                        f32x4{oacc[dt][g * 4] * inv, oacc[dt][g * 4 + 1] * inv,
+                              oacc[dt][g * 4 + 2] * inv, oacc[dt][g * 4 + 3] * inv};
+        }
+        reset();
+    };
+    // Set 0 merges the handed-over partial of block `b` with its own and
+    // writes the result.
+    auto merge_out = [&](int b) {
+        const int row = b ? rowB : rowA;
+        const float l0 = l_part + __shfl_xor(l_part, 32, 64);
+        const float m1 = hand_ml[b][slot][c32][0], l1 = hand_ml[b][slot][c32][1];
+        const float M = fmaxf(m_run, m1);
+        const float mu = M == -INFINITY ? 0.f : M;
+        const float a0 = __builtin_amdgcn_exp2f(m_run - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
+        const float den = l0 * a0 + l1 * a1;
+        const float inv = den > 0.f ? 1.0f / den : 0.f;
+        const float w1 = l1 * a1 * inv, w0 = a0 * inv;
+        const int qrow = row + c32;
+        if (qrow < S) {
+            float *op = out + (int64_t)qrow * q_dim + (int64_t)head * D + h2 * 4;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const f32x4 o1 = __builtin_nontemporal_load((const f32x4 *)(op + dt * 32 + g * 8));
+                    *(f32x4 *)(op + dt * 32 + g * 8) =
+                        f32x4{oacc[dt][g * 4] * w0 + o1[0] * w1, oacc[dt][g * 4 + 1] * w0 + o1[1] * w1,
+                              oacc[dt][g * 4 + 2] * w0 + o1[2] * w1, oacc[dt][g * 4 + 3] * w0 + o1[3] * w1};
+                }
+        }
+        reset();
+    };
+
+    const int nj = (P + 1) / 2;
+    const int jA = (TA - 1) / 2;  // step in which block A's last tile is computed
+    int qblk = task_blk(set) == 1 ? 1 : 0;
+    load_q(qblk ? rowB : rowA);
+    issue(0);
+    issue(1);
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    widen_own(0);
+    widen_own(1);
+    auto step = [&](auto par, int j) {
+        __builtin_amdgcn_s_waitcnt(vm_wait(63) & ~(15 << 8));  // own LDS writes done
+        wg_barrier();  // positions 2j, 2j+1 ready everywhere; 2j-2, 2j-1 consumed
+        issue(2 * j + 2);
+        issue(2 * j + 3);
+        if (set == 0 && j == jA + 1) merge_out(0);
+        const int p = 2 * j + set;
+        const int blk = task_blk(p);
+        if (set == 1 && j == jA && blk != 0) hand_over(0);
+        if (blk >= 0) compute(par, p, blk);
+        if (set == 1 && j == jA && blk == 0) hand_over(0);
+        const int nb = task_blk(p + 2);
+        if (nb >= 0 && nb != qblk) {
+            qblk = nb;
+            load_q(nb ? rowB : rowA);
+        }
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));  // DMA of 2j+2, 2j+3, Q and stores retired
+        widen_own(2 * j + 2);
+        widen_own(2 * j + 3);
+    };
+    for (int j = 0; j < nj; j += 2) {
+        step(Int<0>{}, j);
+        if (j + 1 < nj) step(Int<1>{}, j + 1);
+    }
+    if (set == 1 && gB >= 0) hand_over(1);
+    __builtin_amdgcn_s_waitcnt(vm_wait(0) & ~(15 << 8));
+    wg_barrier();
+    if (set == 0) {
+        if (jA + 1 == nj) merge_out(0);
+        if (gB >= 0) merge_out(1);
+    }
+}
+
 // head_dim 256 keeps the register-staged kernel (the LDS-ring variant needs
 // more than the 256 registers two waves per SIMD allow).
 template <class T, int D, bool V2 = (D <= 128)>
@@ -554,6 +887,12 @@ void PrefillLaunch<T, D, true>::run(const void *q, const void *kc, const void *v
     const int paired = !(win > 0 && win < sp + S);
     const int total = n_units * np;
     const int per_xcd = (total + 7) / 8;
+    if (D <= 128 && kv_mul % 4 == 0 && paired) {
+        hipLaunchKernelGGL((prefill4_kernel<T, D>), dim3(per_xcd * 8), dim3(512), 0, st,
+                           (const uint16_t *)q, (const char *)kc, (const char *)vc, kvs, S, sp,
+                           nh, kv_mul, ng, np, qs, out);
+        return;
+    }
     hipLaunchKernelGGL((prefill2_kernel<T, D>), dim3(per_xcd * 8), dim3(512), 0, st,
                        (const uint16_t *)q, (const char *)kc, (const char *)vc, kvs, S, sp, win,
                        nh, kv_mul, hw, rw, n_units, ng, np, paired, qs, out);
