@@ -102,6 +102,24 @@ __device__ __forceinline__ u32x2 lds_read_tr16_b64(uint32_t a) {
     asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
     return r;
 }
+// 16-byte-per-lane raw buffer load that the compiler does not track: it
+// would otherwise make every later use wait for all vector-memory traffic
+// issued after it (vmcnt retires in order, LDS DMA included).  The caller
+// waits with an explicit vmcnt wait and ties the registers before use.  The
+// resource is a raw descriptor {base lo, base hi, bytes, word3} in SGPRs.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 raw_rsrc(const void *base, int bytes) {
+    const uint64_t v = (uint64_t)base;
+    return i32x4{(int)__builtin_amdgcn_readfirstlane((uint32_t)v),
+                 (int)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32) & 0xffff),
+                 __builtin_amdgcn_readfirstlane(bytes), kRsrcWord3};
+}
+__device__ __forceinline__ u32x4 buffer_load_b128_untracked(const i32x4 &rsrc, int voff) {
+    u32x4 v;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc));
+    return v;
+}
+
 // Same reads with a compile-time byte offset in the instruction's immediate
 // field (0..65535), so per-lane addresses can be computed once.
 template <int OFF>
@@ -117,6 +135,18 @@ __device__ __forceinline__ u32x2 lds_read_tr16_b64_at(uint32_t a) {
     u32x2 r;
     asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
     return r;
+}
+// Waits until at most N LDS reads of this wave are outstanding (they retire
+// in order, so the earlier ones are complete).
+template <int N>
+__device__ __forceinline__ void lds_wait_n() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt");
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
+}
+// max(x[l], x[l ^ 32]) across the wave halves, without an LDS round trip.
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 template <int N>
 __device__ __forceinline__ void lds_wait(u32x4 (&r)[N]) {

@@ -525,22 +525,29 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
 // every step.
 //
 // A workgroup owns 4 heads of one kv head and the causal pair of 32-row
-// blocks A = g, B = NG-1-g.  The key tiles stream in the rotated order
-// 0..TB-1, 0..TA-1 (A on tiles [0, TA), B on [TA, TB) then [0, TA): the online
-// softmax is order-free), two stream positions per step: set 0 (waves 0-3)
-// takes the even positions and set 1 (waves 4-7) the odd ones, each wave
-// keeping its own (m, l, O) for the same 32 query rows of one head.  When a
-// block is done, set 1 hands its partial over -- O/l into the output rows,
-// (m, l) through LDS -- and set 0 merges at the next step.  Every workgroup
-// streams TA+TB tiles, a constant for the causal pair, and no SIMD runs a
-// lone wave.
+// blocks A = g, B = NG-1-g (TA and TB key tiles).  Its TA+TB tile-units are
+// cut into two equal streams: set 0 (waves 0-3) runs A's tiles [0, TA) and
+// then B's tiles [TA, n0); set 1 (waves 4-7) runs B's tiles [n0, TB) and
+// [0, TA).  Every wave keeps (m, l, O) for the 32 query rows of one head.
+// A's output is written by set 0 as soon as its last tile is done; B's two
+// partials (the online softmax is order-free) are merged once after the loop
+// through the idle K/V ring, which also turns the MFMA-layout output into
+// contiguous 2 KiB row stores.  The middle block of an odd block count (no
+// partner) is split the same way.
+//
+// The sets are independent in the main loop: each loads its own stream into
+// its own ring stages and synchronises its 4 waves with an LDS arrival
+// counter, so one set's barrier, DMA and widening overlap the other's MFMAs.
+// Per wave the loop is software-pipelined: step j computes exp(S_j) and the
+// MFMAs of S_{j+1} = QK(j+1), then PV(j) and max(S_{j+1}); K is loaded two
+// items ahead and V one.
 //
 // LDS: K tiles of the 4 ring stages at [0, 4 TILE), V tiles at
-// [4 TILE, 8 TILE).  A wave of set s only reads stages s and s+2, so every
-// per-lane LDS address is fixed at start and the stage, key-row and k-step
-// parts go into the instructions' immediate offsets.  Each wave widens (bf16
-// -> f16) exactly the V bytes its own DMA wrote, so one barrier per step
-// orders DMA, widening and reads.
+// [4 TILE, 8 TILE); set s's item i lives in stage 2 (i & 1) + s.  Every
+// per-lane LDS address is therefore fixed at start and the stage, key-row and
+// k-step parts go into the instructions' immediate offsets.  Each wave widens
+// (bf16 -> f16) exactly the V bytes its own DMA wrote, so the one set barrier
+// per step orders DMA, widening and reads.
 //
 // The running max is raised only when a row's tile max exceeds it by more
 // than 2^8 (in the exp2 domain): P = exp2(s - m) then stays <= 256, exact in
@@ -557,15 +564,19 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     constexpr int NSTG = 4, VREG = NSTG * TILE;
     constexpr bool CVTV = __is_same(T, BF16);
     constexpr float kLazy = 8.0f;  // log2 headroom before the max is raised
+    constexpr int OROW = 4 * D * 4;  // staged output row: 4 heads of f32
+    constexpr int CPR = OROW / 16;    // its 16-byte chunks, stored at chunk ^ (row & 15)
     static_assert(D <= 128 && BN == 64, "v4 tiling");
     static_assert(2 * TILE + (NKT * 32) * RB <= 65535, "immediate offsets");
+    static_assert(4 * 64 * NDT * 64 + 32 * OROW <= 2 * VREG, "epilogue staging");
     // 16-byte slot swizzle of key row r.  A 256-byte row (D = 128) spans all
     // 64 banks, so the four rows one 16-lane transpose read touches must land
     // on different slot pairs: XOR with 2r, not r.  128-byte rows (D = 64)
     // alternate bank halves and use r itself.
     auto swz = [](int r) { return D == 128 ? (r << 1) & (SLOTS - 1) : r & (SLOTS - 1); };
     __shared__ __attribute__((aligned(1024))) char lds[2 * VREG];
-    __shared__ float hand_ml[2][4][32][2];
+    __shared__ float hand_ml[4][32][2];
+    __shared__ uint32_t set_bar[2];
 
     const int n_units = (n_head / kv_mul) * (kv_mul / 4);
     const int total = n_units * np;
@@ -585,60 +596,76 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     const int64_t q_dim = (int64_t)n_head * D;
     const int head = head0 + slot;
 
-    const int rowA = gA * 32, rowB = gB >= 0 ? gB * 32 : S;
-    auto tiles_hi = [&](int row) {
-        return row < S ? (start_pos + min(row + 32, S) + BN - 1) / BN : 0;
-    };
-    const int TA = tiles_hi(rowA), TB = tiles_hi(rowB);
-    const int TB1 = max(TB, TA);
-    const int P = TB1 + (TB > 0 ? TA : 0);
-    auto stream_tile = [&](int p) { return p < TB1 ? p : p - TB1; };
-    auto task_blk = [&](int p) {  // 0 = A, 1 = B, -1 = idle
-        if (p >= P) return -1;
-        const int t = stream_tile(p);
-        if (p < TB1) return t < TA ? 0 : (t < TB ? 1 : -1);
-        return t < TA ? 1 : -1;
+    // ---- the two tile streams ----
+    const int rowA = gA * 32, rowB = gB >= 0 ? gB * 32 : rowA;  // rowB: merged block
+    const int TA = (start_pos + min(rowA + 32, S) + BN - 1) / BN;
+    const int TB = gB >= 0 ? (start_pos + min(rowB + 32, S) + BN - 1) / BN : 0;
+    const int n_tot = TA + TB;
+    const int n0 = (n_tot + 1) / 2, n1 = n_tot - n0;
+    // item i of stream s -> key tile, and whether it belongs to block A
+    // (only set 0 has A items when the block has a partner).
+    auto item_tile = [&](int s_, int i) {
+        if (gB < 0) return s_ ? n0 + i : i;
+        if (s_ == 0) return i;
+        const int t = n0 + i;
+        return t < TB ? t : t - TB;
     };
 
-    // ---- K/V DMA (each wave loads NIW 1 KiB chunks of every K and V tile) ----
+    const int n_me = set ? n1 : n0;
+
+    // ---- K/V DMA: each set loads its own stream, NIWS 1 KiB chunks per wave ----
+    constexpr int NIWS = 2 * NIW;
     const int rbg = (int)(kv_stride * 2);
     const int range = (kv_len - 1) * rbg + D * 2;
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t vrs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
-    int dofs[NIW];
+    int dofs[NIWS];
 #pragma unroll
-    for (int i = 0; i < NIW; i++) {
-        const int r = (wave * NIW + i) * RPI + lane / SLOTS;
+    for (int i = 0; i < NIWS; i++) {
+        const int r = (slot * NIWS + i) * RPI + lane / SLOTS;
         dofs[i] = r * rbg + (((lane % SLOTS) ^ swz(r)) * 16);
     }
-    auto issue = [&](int p) {
-        const int t = p < P ? stream_tile(p) : (kv_len + BN) / BN;  // past P: zeros
+    // This wave's chunks of item i of its set's stream: K (kv = 0) or V (kv = 1).
+    auto load_tile = [&](int kv, int i) {
+        const int t = i < n_me ? item_tile(set, i) : (kv_len + BN) / BN;  // past: zeros
         const int so = t * BN * rbg;
-        char *st = lds + (p % NSTG) * TILE;
+        char *st = lds + kv * VREG + (2 * (i & 1) + set) * TILE + slot * NIWS * 1024;
 #pragma unroll
-        for (int i = 0; i < NIW; i++) {
-            dma16(krs, st + (wave * NIW + i) * 1024, dofs[i] + so, 0);
-            dma16(vrs, st + VREG + (wave * NIW + i) * 1024, dofs[i] + so, 0);
-        }
+        for (int c = 0; c < NIWS; c++) dma16(kv ? vrs : krs, st + c * 1024, dofs[c] + so, 0);
     };
-    auto widen_own = [&](int p) {
+    // bf16 -> f16 in place, for the V chunks this wave loaded of item j + 1.
+    auto widen_own = [&](int j) {
         if constexpr (CVTV) {
-            const uint32_t vb = lds_addr(lds + VREG + (p % NSTG) * TILE) + wave * NIW * 1024 + lane * 16;
-            u32x4 w[NIW];
+            const uint32_t vb = lds_addr(lds + VREG + (2 * ((j + 1) & 1) + set) * TILE) +
+                                slot * NIWS * 1024 + lane * 16;
+            u32x4 w[NIWS];
 #pragma unroll
-            for (int i = 0; i < NIW; i++) w[i] = lds_read_b128(vb + i * 1024);
+            for (int i = 0; i < NIWS; i++) w[i] = lds_read_b128(vb + i * 1024);
             lds_wait_any();
 #pragma unroll
-            for (int i = 0; i < NIW; i++) {
+            for (int i = 0; i < NIWS; i++) {
                 tie(w[i]);
                 u32x4 o;
 #pragma unroll
-                for (int j = 0; j < 4; j++) o[j] = pack_f16x2(bf16_lo(w[i][j]), bf16_hi(w[i][j]));
+                for (int e = 0; e < 4; e++) o[e] = pack_f16x2(bf16_lo(w[i][e]), bf16_hi(w[i][e]));
                 lds_write_b128(vb + i * 1024, o);
             }
         }
+    };
+    // Barrier of the 4 waves of this set (the sets run independently in the
+    // main loop): a monotonic LDS arrival counter.  Callers have retired
+    // their DMA (vmcnt) and LDS writes (lgkmcnt) before arriving.
+    uint32_t bar_target = 0;
+    auto set_barrier = [&]() {
+        bar_target += 4;
+        asm volatile("" ::: "memory");
+        if (lane == 0)
+            __hip_atomic_fetch_add(&set_bar[set], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        while (__hip_atomic_load(&set_bar[set], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < bar_target)
+            __builtin_amdgcn_s_sleep(1);
+        asm volatile("" ::: "memory");
     };
 
     // ---- fixed per-lane LDS read addresses (stage `set`, key row 0) ----
@@ -659,15 +686,20 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
             va_addr[dt][h] = lds0 + VREG + set * TILE + R * RB + ((chq ^ swz(R)) * 16) + boff;
         }
 
-    // ---- Q of the block being computed (reloaded once, at the A -> B switch) ----
-    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
-        uniform_ptr(q), 0, (int)((int64_t)S * q_dim * 2), kRsrcWord3);
+    // ---- Q of the block being computed (set 0 reloads once, at A -> B) ----
+    // Untracked loads: the reload at the A -> B switch would otherwise make
+    // every QK MFMA wait for the step's K/V DMA.  Each load_q is followed by
+    // a vmcnt(0) wait and tie_q before the next QK.
+    const i32x4 qrs = raw_rsrc(q, (int)((int64_t)S * q_dim * 2));
     u32x4 qv[NKS];
     auto load_q = [&](int row) {
         const int o = (int)((min(row + c32, S) * q_dim + (int64_t)head * D + h2 * 8) * 2);
 #pragma unroll
-        for (int s = 0; s < NKS; s++)
-            qv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qrs, o + s * 32, 0, 0));
+        for (int s = 0; s < NKS; s++) qv[s] = buffer_load_b128_untracked(qrs, o + s * 32);
+    };
+    auto tie_q = [&]() {
+#pragma unroll
+        for (int s = 0; s < NKS; s++) tie(qv[s]);
     };
 
     f32x16 oacc[NDT];
@@ -675,42 +707,64 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
     float m_run = -INFINITY, l_part = 0.f;
 
-    auto compute = [&](auto par, int p, int blk) {
-        constexpr int SOFF = decltype(par)::value * 2 * TILE;  // stage s or s+2
-        const int row = blk ? rowB : rowA;
-        const int kb = stream_tile(p) * BN;
-        f32x16 sacc[NKT];
-        static_for<0, NKT>([&](auto ktc) {
-            constexpr int kt = decltype(ktc)::value;
-            u32x4 ka[NKS];
-            static_for<0, NKS>([&](auto sc) {
-                constexpr int s = decltype(sc)::value;
-                ka[s] = lds_read_b128_at<SOFF + kt * 32 * RB>(ka_addr[s]);
+    // S of two consecutive items: item i lives in s2[i & 1].
+    f32x16 s2[2][NKT];
+    u32x4 ph[NKT][2];  // P (f16) of the item awaiting PV
+    // S = K Q^T of the item in K stage 2 KPAR + set, into s2[DST].  The K
+    // reads run two groups of G ahead of the MFMAs that use them.
+    auto qk = [&](auto kparc, auto dstc) {
+        constexpr int SOFF = decltype(kparc)::value * 2 * TILE, DST = decltype(dstc)::value;
+        constexpr int G = 4, NG = NKT * NKS / G;
+        u32x4 kbuf[2][G];
+        auto rd = [&](auto gc) {
+            constexpr int g = decltype(gc)::value, kt = g * G / NKS, s0 = g * G % NKS;
+            static_for<0, G>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                kbuf[g & 1][i] = lds_read_b128_at<SOFF + kt * 32 * RB>(ka_addr[s0 + i]);
             });
-            lds_wait_any();
-            sacc[kt] = f32x16{};
+        };
+        rd(Int<0>{});
+        rd(Int<1>{});
+        static_for<0, NG>([&](auto gc) {
+            constexpr int g = decltype(gc)::value, kt = g * G / NKS, s0 = g * G % NKS;
+            lds_wait_n<(g + 1 < NG ? G : 0)>();
+            if constexpr (s0 == 0) s2[DST][kt] = f32x16{};
 #pragma unroll
-            for (int s = 0; s < NKS; s++) {
-                tie(ka[s]);
-                sacc[kt] = mfma32<T>(ka[s], qv[s], sacc[kt]);
+            for (int i = 0; i < G; i++) {
+                tie(kbuf[g & 1][i]);
+                s2[DST][kt] = mfma32<T>(kbuf[g & 1][i], qv[s0 + i], s2[DST][kt]);
             }
+            if constexpr (g + 2 < NG) rd(Int<g + 2>{});
         });
-        const int pos_row = start_pos + row + c32;
-        if (kb + BN - 1 > start_pos + row) {  // tile reaches past the block's first row
+    };
+    // Causal mask of s2[SRC] for key tile `tile` and query block `row`
+    // (only the tiles that reach past the block's first row need it).
+    auto mask = [&](auto srcc, int row, int tile) {
+        constexpr int SRC = decltype(srcc)::value;
+        const int kb = tile * BN;
+        if (kb + BN - 1 > start_pos + row) {
+            const int pos_row = start_pos + row + c32;
 #pragma unroll
             for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int key = kb + kt * 32 + (i >> 2) * 8 + h2 * 4 + (i & 3);
-                    sacc[kt][i] = key > pos_row ? -INFINITY : sacc[kt][i];
+                    s2[SRC][kt][i] = key > pos_row ? -INFINITY : s2[SRC][kt][i];
                 }
         }
+    };
+    // Row max of s2[SRC], in the exp2 domain.
+    auto rowmax = [&](auto srcc) {
+        constexpr int SRC = decltype(srcc)::value;
         float mloc = -INFINITY;
 #pragma unroll
         for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) mloc = fmaxf(mloc, sacc[kt][i]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * qscale;
+            for (int i = 0; i < 16; i++) mloc = fmaxf(mloc, s2[SRC][kt][i]);
+        return max_xor32(mloc) * qscale;
+    };
+    // Lazy online-softmax max update before an item's exponentials.
+    auto raise_max = [&](float mloc) {
         if (__any(mloc > m_run + kLazy)) {
             const float m_new = fmaxf(m_run, mloc);
             const float corr = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
@@ -719,136 +773,195 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
             for (int dt = 0; dt < NDT; dt++) oacc[dt] *= corr;
             m_run = m_new;
         }
+    };
+    // P = exp2(S scale - m) of s2[SRC] as f16, and l += sum(P) in f32.
+    auto exps = [&](auto srcc) {
+        constexpr int SRC = decltype(srcc)::value;
         const float mu = m_run == -INFINITY ? 0.f : m_run;
-        u32x4 ph[NKT][2];
 #pragma unroll
         for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
             for (int ks = 0; ks < 2; ks++)
 #pragma unroll
                 for (int jj = 0; jj < 4; jj++) {
-                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][ks * 8 + 2 * jj], qscale, -mu));
-                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][ks * 8 + 2 * jj + 1], qscale, -mu));
-                    l_part += p0 + p1;
+                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s2[SRC][kt][ks * 8 + 2 * jj], qscale, -mu));
+                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s2[SRC][kt][ks * 8 + 2 * jj + 1], qscale, -mu));
                     ph[kt][ks][jj] = pack_f16x2(p0, p1);
+                    l_part += p0 + p1;
                 }
-        static_for<0, NDT>([&](auto dtc) {
+    };
+    // O += V^T P with the item's V in V stage 2 VPAR + set.  The V^T reads of
+    // d tile dt + 1 are in flight during dt's MFMAs.
+    auto pv = [&](auto vparc) {
+        constexpr int SOFF = decltype(vparc)::value * 2 * TILE;
+        constexpr int RPD = NKT * 2 * 2;  // transpose reads per d tile
+        u32x2 vbuf[2][NKT][2][2];
+        auto rd = [&](auto dtc) {
             constexpr int dt = decltype(dtc)::value;
-            u32x4 va[NKT][2];
             static_for<0, NKT>([&](auto ktc) {
                 constexpr int kt = decltype(ktc)::value;
                 static_for<0, 2>([&](auto ksc) {
                     constexpr int ks = decltype(ksc)::value;
                     constexpr int off = SOFF + (kt * 32 + ks * 16) * RB;
-                    const u32x2 a0 = lds_read_tr16_b64_at<off>(va_addr[dt][0]);
-                    const u32x2 a1 = lds_read_tr16_b64_at<off>(va_addr[dt][1]);
-                    va[kt][ks] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+                    vbuf[dt & 1][kt][ks][0] = lds_read_tr16_b64_at<off>(va_addr[dt][0]);
+                    vbuf[dt & 1][kt][ks][1] = lds_read_tr16_b64_at<off>(va_addr[dt][1]);
                 });
             });
-            lds_wait_any();
+        };
+        rd(Int<0>{});
+        if constexpr (NDT > 1) rd(Int<1>{});
+        static_for<0, NDT>([&](auto dtc) {
+            constexpr int dt = decltype(dtc)::value;
+            lds_wait_n<(dt + 1 < NDT ? RPD : 0)>();
 #pragma unroll
             for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
                 for (int ks = 0; ks < 2; ks++) {
-                    tie(va[kt][ks]);
-                    oacc[dt] = mfma32<F16>(va[kt][ks], ph[kt][ks], oacc[dt]);
+                    tie(vbuf[dt & 1][kt][ks][0]);
+                    tie(vbuf[dt & 1][kt][ks][1]);
+                    const u32x2 a0 = vbuf[dt & 1][kt][ks][0], a1 = vbuf[dt & 1][kt][ks][1];
+                    oacc[dt] = mfma32<F16>(u32x4{a0[0], a0[1], a1[0], a1[1]}, ph[kt][ks], oacc[dt]);
                 }
+            if constexpr (dt + 2 < NDT) rd(Int<dt + 2>{});
         });
     };
 
-    auto reset = [&]() {
-#pragma unroll
-        for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
-        m_run = -INFINITY;
-        l_part = 0.f;
-    };
-    // Set 1 hands its partial of block `b` to set 0: O/l into the output rows
-    // (f32), (m, l) into LDS.
-    auto hand_over = [&](int b) {
-        const int row = b ? rowB : rowA;
-        const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
-        const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-        const int qrow = row + c32;
-        if (h2 == 0) { hand_ml[b][slot][c32][0] = m_run; hand_ml[b][slot][c32][1] = l_tot; }
-        if (qrow < S) {
-            float *op = out + (int64_t)qrow * q_dim + (int64_t)head * D + h2 * 4;
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-                for (int g = 0; g < 4; g++)
-                    *(f32x4 *)(op + dt * 32 + g * 8) =
-                        f32x4{oacc[dt][g * 4] * inv, oacc[dt][g * 4 + 1] * inv,
-                              oacc[dt][g * 4 + 2] * inv, oacc[dt][g * 4 + 3] * inv};
+    // ---- main loop ----
+    // Software pipeline per wave: step j runs exp(S_j) interleaved with the
+    // MFMAs of S_{j+1} = QK(j+1), then PV(j) interleaved with max(S_{j+1}).
+    // K is therefore loaded two items ahead and V one: step j loads K of
+    // item j+2 (into item j's K stage) and V of item j+1.
+    auto row_of = [&](int i) { return set == 0 && gB >= 0 && i < TA ? rowA : rowB; };
+    if (tid < 2) set_bar[tid] = 0;
+    load_q(set == 0 ? rowA : rowB);
+    load_tile(0, 0);
+    load_tile(0, 1);
+    load_tile(1, 0);
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    tie_q();
+    widen_own(-1);
+    __builtin_amdgcn_s_waitcnt(vm_wait(63) & ~(15 << 8));
+    wg_barrier();
+    if (n_me > 0) {
+        qk(Int<0>{}, Int<0>{});
+        mask(Int<0>{}, row_of(0), item_tile(set, 0));
+        raise_max(rowmax(Int<0>{}));
+        if (set == 0 && gB >= 0 && TA == 1) {
+            load_q(rowB);
+            __builtin_amdgcn_s_waitcnt(vm_wait(0));
+            tie_q();
         }
-        reset();
+    }
+    auto step = [&](auto par, int j) {
+        constexpr int P = decltype(par)::value;
+        constexpr Int<P ^ 1> npar{};
+        __builtin_amdgcn_s_waitcnt(vm_wait(63) & ~(15 << 8));  // own LDS writes done
+        set_barrier();  // item j's V and item j+1's K ready; item j's K and j-1's V consumed
+        load_tile(0, j + 2);
+        {
+            exps(par);
+            qk(npar, npar);  // item j+1 (an idle tile of zeros past the end)
+            if (set == 0 && gB >= 0 && j + 1 == TA - 1) load_q(rowB);
+        }
+        load_tile(1, j + 1);
+        {
+            mask(npar, row_of(j + 1), item_tile(set, j + 1));
+            pv(par);
+            const float m_next = rowmax(npar);
+            if (set == 0 && gB >= 0 && j == TA - 1) {  // block A complete: write it, switch to B
+                const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+                const float inv = 1.0f / l_tot;
+                const int qrow = rowA + c32;
+                if (qrow < S) {
+                    float *op = out + (int64_t)qrow * q_dim + (int64_t)head * D + h2 * 4;
+#pragma unroll
+                    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                        for (int g = 0; g < 4; g++)
+                            __builtin_nontemporal_store(
+                                f32x4{oacc[dt][g * 4] * inv, oacc[dt][g * 4 + 1] * inv,
+                                      oacc[dt][g * 4 + 2] * inv, oacc[dt][g * 4 + 3] * inv},
+                                (f32x4 *)(op + dt * 32 + g * 8));
+                }
+#pragma unroll
+                for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
+                m_run = -INFINITY;
+                l_part = 0.f;
+            }
+            if (j + 1 < n_me) raise_max(m_next);
+        }
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));  // item j+2's K, j+1's V, Q and stores retired
+        tie_q();
+        widen_own(j);
     };
-    // Set 0 merges the handed-over partial of block `b` with its own and
-    // writes the result.
-    auto merge_out = [&](int b) {
-        const int row = b ? rowB : rowA;
+    for (int j = 0; j < n_me; j += 2) {
+        step(Int<0>{}, j);
+        if (j + 1 < n_me) step(Int<1>{}, j + 1);
+    }
+
+    // ---- merge the merged block's two partials through LDS ----
+    __builtin_amdgcn_s_waitcnt(vm_wait(0) & ~(15 << 8));
+    wg_barrier();  // ring idle
+    const uint32_t part = lds0 + (slot * 64 + lane) * 16;  // [slot][dt][g][lane] f32x4
+    if (set == 1) {
+        const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+        if (h2 == 0) { hand_ml[slot][c32][0] = m_run; hand_ml[slot][c32][1] = l_tot; }
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                lds_write_b128(part + (dt * 4 + g) * 4 * 64 * 16,
+                               __builtin_bit_cast(u32x4, f32x4{oacc[dt][g * 4], oacc[dt][g * 4 + 1],
+                                                               oacc[dt][g * 4 + 2], oacc[dt][g * 4 + 3]}));
+    }
+    __builtin_amdgcn_s_waitcnt(vm_wait(63) & ~(15 << 8));
+    wg_barrier();
+    const uint32_t stg = lds0 + 4 * 64 * NDT * 64;  // staged rows [32][OROW]
+    if (set == 0) {
         const float l0 = l_part + __shfl_xor(l_part, 32, 64);
-        const float m1 = hand_ml[b][slot][c32][0], l1 = hand_ml[b][slot][c32][1];
+        const float m1 = hand_ml[slot][c32][0], l1 = hand_ml[slot][c32][1];
         const float M = fmaxf(m_run, m1);
         const float mu = M == -INFINITY ? 0.f : M;
         const float a0 = __builtin_amdgcn_exp2f(m_run - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
         const float den = l0 * a0 + l1 * a1;
         const float inv = den > 0.f ? 1.0f / den : 0.f;
-        const float w1 = l1 * a1 * inv, w0 = a0 * inv;
-        const int qrow = row + c32;
-        if (qrow < S) {
-            float *op = out + (int64_t)qrow * q_dim + (int64_t)head * D + h2 * 4;
+        const float w0 = a0 * inv, w1 = a1 * inv;
+        u32x4 o1[NDT][4];
 #pragma unroll
-            for (int dt = 0; dt < NDT; dt++)
+        for (int dt = 0; dt < NDT; dt++)
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const f32x4 o1 = __builtin_nontemporal_load((const f32x4 *)(op + dt * 32 + g * 8));
-                    *(f32x4 *)(op + dt * 32 + g * 8) =
-                        f32x4{oacc[dt][g * 4] * w0 + o1[0] * w1, oacc[dt][g * 4 + 1] * w0 + o1[1] * w1,
-                              oacc[dt][g * 4 + 2] * w0 + o1[2] * w1, oacc[dt][g * 4 + 3] * w0 + o1[3] * w1};
-                }
-        }
-        reset();
-    };
-
-    const int nj = (P + 1) / 2;
-    const int jA = (TA - 1) / 2;  // step in which block A's last tile is computed
-    int qblk = task_blk(set) == 1 ? 1 : 0;
-    load_q(qblk ? rowB : rowA);
-    issue(0);
-    issue(1);
-    __builtin_amdgcn_s_waitcnt(vm_wait(0));
-    widen_own(0);
-    widen_own(1);
-    auto step = [&](auto par, int j) {
-        __builtin_amdgcn_s_waitcnt(vm_wait(63) & ~(15 << 8));  // own LDS writes done
-        wg_barrier();  // positions 2j, 2j+1 ready everywhere; 2j-2, 2j-1 consumed
-        issue(2 * j + 2);
-        issue(2 * j + 3);
-        if (set == 0 && j == jA + 1) merge_out(0);
-        const int p = 2 * j + set;
-        const int blk = task_blk(p);
-        if (set == 1 && j == jA && blk != 0) hand_over(0);
-        if (blk >= 0) compute(par, p, blk);
-        if (set == 1 && j == jA && blk == 0) hand_over(0);
-        const int nb = task_blk(p + 2);
-        if (nb >= 0 && nb != qblk) {
-            qblk = nb;
-            load_q(nb ? rowB : rowA);
-        }
-        __builtin_amdgcn_s_waitcnt(vm_wait(0));  // DMA of 2j+2, 2j+3, Q and stores retired
-        widen_own(2 * j + 2);
-        widen_own(2 * j + 3);
-    };
-    for (int j = 0; j < nj; j += 2) {
-        step(Int<0>{}, j);
-        if (j + 1 < nj) step(Int<1>{}, j + 1);
+            for (int g = 0; g < 4; g++) o1[dt][g] = lds_read_b128(part + (dt * 4 + g) * 4 * 64 * 16);
+        lds_wait_any();
+        const uint32_t dst = stg + c32 * OROW;
+        const int c0 = slot * (D / 4) + h2;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                tie(o1[dt][g]);
+                const f32x4 b = __builtin_bit_cast(f32x4, o1[dt][g]);
+                lds_write_b128(dst + ((c0 + dt * 8 + g * 2) ^ (c32 & 15)) * 16,
+                               __builtin_bit_cast(u32x4, f32x4{oacc[dt][g * 4] * w0 + b[0] * w1,
+                                                               oacc[dt][g * 4 + 1] * w0 + b[1] * w1,
+                                                               oacc[dt][g * 4 + 2] * w0 + b[2] * w1,
+                                                               oacc[dt][g * 4 + 3] * w0 + b[3] * w1}));
+            }
     }
-    if (set == 1 && gB >= 0) hand_over(1);
-    __builtin_amdgcn_s_waitcnt(vm_wait(0) & ~(15 << 8));
+    __builtin_amdgcn_s_waitcnt(vm_wait(63) & ~(15 << 8));
     wg_barrier();
-    if (set == 0) {
-        if (jA + 1 == nj) merge_out(0);
-        if (gB >= 0) merge_out(1);
+    // 32 rows x (4 heads x D f32), contiguous in the output row: 8 waves x 4 rows.
+#pragma unroll
+    for (int r4 = 0; r4 < 4; r4++) {
+        const int r = wave * 4 + r4;
+        const int qrow = rowB + r;
+#pragma unroll
+        for (int c = lane; c < CPR; c += 64) {
+            const u32x4 v = lds_read_b128(stg + r * OROW + (c ^ (r & 15)) * 16);
+            lds_wait_any();
+            if (qrow < S)
+                __builtin_nontemporal_store(__builtin_bit_cast(f32x4, v),
+                                            (f32x4 *)(out + (int64_t)qrow * q_dim + (int64_t)head0 * D) + c);
+        }
     }
 }
 
