@@ -9,24 +9,23 @@
 // caps one CU far below its share of HBM bandwidth.  Here both contractions
 // run on v_mfma_f32_16x16x32_{f16,bf16} and the VALU only does the softmax:
 //  * A "unit" is up to 16 query heads sharing one kv head (GQA group).
-//  * S^T[16 keys x 16 heads] = K . Q^T: the K tile is the A operand and comes
-//    straight from 16-byte global loads (lane = key, 8 consecutive d); Q^T is
-//    the B operand, held in registers for the whole call.  q (f32) is split
-//    into hi + lo halves of the cache dtype, two MFMAs per step, so the
-//    product keeps ~f32 accuracy.
-//  * O^T[16 d x 16 heads] += V^T . P^T: V^T is the A operand.  Each lane
-//    loads 8 keys x 8 d of V, transposes them in registers and stores them in
-//    a wave-private LDS tile [d][key]; one 16-byte LDS read per d tile then
-//    gives the operand.  P^T (the B operand) is exactly the S^T accumulator of
-//    two key tiles, exponentiated: the key order inside a k-step is free, so
-//    the LDS tile is written in accumulator order and P never moves between
-//    lanes.  f16 caches use P in f16 (2^-11); bf16 caches split P into
-//    hi + lo bf16 (two MFMAs) to stay inside a 1e-3 rel-L2 budget.
+//  * S^T[16 keys x 16 heads] = K . Q^T: K is the A operand, Q^T the B operand
+//    held in registers for the whole call.  q (f32) is split into hi + lo
+//    halves of the cache dtype, two MFMAs per step, so the product keeps
+//    ~f32 accuracy.
+//  * O^T[16 d x 16 heads] += V^T . P^T: V^T is the A operand, read from a
+//    row-major LDS tile by the transposing ds_read_b64_tr_b16.  P^T (the B
+//    operand) is exactly the S^T accumulator of two key tiles, exponentiated:
+//    the key order inside a k-step is free, so P never moves between lanes.
+//    f16 caches use P in f16 (2^-11); bf16 caches split P into hi + lo bf16
+//    (two MFMAs) to stay inside a 1e-3 rel-L2 budget.
 //  * In both accumulators a lane's column is one head, so the running max,
 //    sum and rescale of a head live in the lanes that own its output.
-//  * Waves of a workgroup stream disjoint key blocks and merge through LDS;
-//    splits merge in-launch: the last workgroup of a unit (agent-scope
-//    counter) combines the partials and writes `out`.
+//  * head_dim <= 128 streams K/V tiles global -> LDS by buffer_load ... lds
+//    (decode_dma_kernel, 1 or 4 waves per workgroup); head_dim 256 stages
+//    through registers (decode_mfma_kernel).
+//  * The waves of a workgroup stream disjoint key blocks and combine through
+//    LDS; the splits of a unit are combined by decode_merge_kernel.
 #include <cstdlib>
 #include "common.hpp"
 #include "mfma_util.hpp"
@@ -38,6 +37,44 @@ constexpr int kMW = 4;          // waves per workgroup
 constexpr int kTok = 32;        // keys per wave iteration (two 16-key tiles)
 constexpr int kMaxUnitHeads = 16;
 constexpr int kMfmaTargetWG = 256;  // one 4-wave workgroup per CU (LDS-bound)
+
+// Finishes one (sequence, unit) split after its waves have staged their
+// (m, l, O) in LDS (sm_m, sm_l: [MW][16]; sm_o: [MW][16][D + 4]): combines
+// the waves; with one split writes `out`, otherwise writes the split's
+// partial (O unnormalised, m, l) for decode_merge_kernel.
+template <int D, int MW = kMW>
+__device__ void finish_unit(const float *sm_m, const float *sm_l, const float *sm_o, int b,
+                            int unit, int split, int splits, int gt, int n_units, int n_head,
+                            int head0, float *__restrict__ out, float *__restrict__ ws_ml,
+                            float *__restrict__ ws_acc) {
+    constexpr int NT = MW * 64;
+    const int tid = threadIdx.x;
+    const int64_t u = (int64_t)b * n_units + unit;
+    const int GD = gt * D;
+    for (int idx = tid; idx < GD; idx += NT) {
+        const int g = idx / D, d = idx % D;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < MW; w++) mx = fmaxf(mx, sm_m[w * 16 + g]);
+        const float mu = mx == -INFINITY ? 0.f : mx;
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (int w = 0; w < MW; w++) {
+            const float c = __builtin_amdgcn_exp2f(sm_m[w * 16 + g] - mu);
+            num += sm_o[(w * 16 + g) * (D + 4) + d] * c;
+            den += sm_l[w * 16 + g] * c;
+        }
+        if (splits == 1) {
+            out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
+        } else {
+            ws_acc[(u * splits + split) * GD + idx] = num;
+            if (d == 0) {
+                ws_ml[((u * splits + split) * gt + g) * 2] = mx;
+                ws_ml[((u * splits + split) * gt + g) * 2 + 1] = den;
+            }
+        }
+    }
+}
 
 template <class T, int D>
 __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel(
@@ -252,39 +289,17 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     float *sm = (float *)&vt_all[0][0];
     float *sm_m = sm;                                 // [kMW][16]
     float *sm_l = sm + kMW * 16;                      // [kMW][16]
-    float *sm_o = sm + 2 * kMW * 16;                  // [kMW][16][D]
+    float *sm_o = sm + 2 * kMW * 16;                  // [kMW][16][D + 4]
     if (kg == 0) { sm_m[wave * 16 + n16] = m_run; sm_l[wave * 16 + n16] = l_part; }
+    // Row pitch D + 4 floats: the 16 heads of a lane group land on different
+    // banks (a pitch of D would put them all on one).
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) sm_o[(wave * 16 + n16) * D + dt * 16 + kg * 4 + i] = oacc[dt][i];
+        *(f32x4 *)&sm_o[(wave * 16 + n16) * (D + 4) + dt * 16 + kg * 4] = oacc[dt];
     __syncthreads();
 
-    const int64_t u = (int64_t)b * n_units + unit;
-    const int GD = gt * D;
-    for (int idx = tid; idx < GD; idx += kMW * 64) {
-        const int g = idx / D, d = idx % D;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kMW; w++) mx = fmaxf(mx, sm_m[w * 16 + g]);
-        const float mu = mx == -INFINITY ? 0.f : mx;
-        float num = 0.f, den = 0.f;
-#pragma unroll
-        for (int w = 0; w < kMW; w++) {
-            const float c = exp2f(sm_m[w * 16 + g] - mu);
-            num += sm_o[(w * 16 + g) * D + d] * c;
-            den += sm_l[w * 16 + g] * c;
-        }
-        if (splits == 1) {
-            out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
-        } else {
-            ws_acc[(u * splits + split) * GD + idx] = num;
-            if (d == 0) {
-                ws_ml[((u * splits + split) * gt + g) * 2] = mx;
-                ws_ml[((u * splits + split) * gt + g) * 2 + 1] = den;
-            }
-        }
-    }
+    finish_unit<D>(sm_m, sm_l, sm_o, b, unit, split, splits, gt, n_units, n_head, head0, out,
+                   ws_ml, ws_acc);
 }
 
 }  // namespace ullm
@@ -301,8 +316,8 @@ namespace ullm {
 // wave owns two stages (double buffering); the wait for a stage leaves the
 // other stage's transfers in flight.
 
-template <class T, int D>
-__global__ __launch_bounds__(kMW * 64, 1) void decode_dma_kernel(
+template <class T, int D, int MW>
+__global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
     int n_head, int kv_mul, int gt, int n_units, int chunk, int splits, float qscale,
@@ -328,8 +343,8 @@ __global__ __launch_bounds__(kMW * 64, 1) void decode_dma_kernel(
     // One array per stage: the stage a read targets is then a distinct
     // object from the stage the DMA is filling, which keeps the compiler from
     // draining all DMA (vmcnt(0)) before every LDS read.
-    __shared__ __attribute__((aligned(1024))) char lds0[kMW * STAGE];
-    __shared__ __attribute__((aligned(1024))) char lds1[kMW * STAGE];
+    __shared__ __attribute__((aligned(1024))) char lds0[MW * STAGE];
+    __shared__ __attribute__((aligned(1024))) char lds1[MW * STAGE];
     char *const wb0 = lds0 + wave * STAGE;
     char *const wb1 = lds1 + wave * STAGE;
 
@@ -366,13 +381,7 @@ __global__ __launch_bounds__(kMW * 64, 1) void decode_dma_kernel(
             dma16(vrs, vt + i * 1024, dofs[i] + so, 0);
     };
 
-    constexpr int STEP = kMW * kTok;
-    const int tb0 = c0 + wave * kTok;
-    issue(wb0, tb0);
-    issue(wb1, tb0 + STEP);
-
-    // q is loaded after the first two DMA stages are queued; vmcnt retires in
-    // order, so waiting for q also waits for data the first block needs.
+    // q goes out first: waiting for it then leaves the K/V stages in flight.
     f32x4 qa[NS][2];
     {
         const float *qp = q + ((int64_t)b * n_head + head0 + (head_ok ? n16 : 0)) * D;
@@ -382,7 +391,12 @@ __global__ __launch_bounds__(kMW * 64, 1) void decode_dma_kernel(
             qa[s][1] = *(const f32x4 *)(qp + (s * 4 + kg) * 8 + 4);
         }
     }
-
+    // Stages are issued only for keys that exist (a wave with one block
+    // issues one stage); the waits below count exactly what was issued.
+    constexpr int STEP = MW * kTok;
+    const int tb0 = c0 + wave * kTok;
+    if (tb0 < c1) issue(wb0, tb0);
+    if (tb0 + STEP < c1) issue(wb1, tb0 + STEP);
 
     u32x4 qh[NS], ql[NS];
 #pragma unroll
@@ -488,54 +502,34 @@ __global__ __launch_bounds__(kMW * 64, 1) void decode_dma_kernel(
     // have retired (lgkmcnt(0)), two blocks ahead.
     constexpr int kLgkm0 = vm_wait(63) & ~(15 << 8);
     for (int tb = tb0; tb < c1; tb += 2 * STEP) {
-        __builtin_amdgcn_s_waitcnt(vm_wait(2 * NI));  // stage 0 landed, stage 1 in flight
+        if (tb + STEP < c1) __builtin_amdgcn_s_waitcnt(vm_wait(2 * NI));  // stage 1 in flight
+        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
         consume(wb0, tb);
         __builtin_amdgcn_s_waitcnt(kLgkm0);
-        issue(wb0, tb + 2 * STEP);
+        if (tb + 2 * STEP < c1) issue(wb0, tb + 2 * STEP);
         if (tb + STEP >= c1) break;
-        __builtin_amdgcn_s_waitcnt(vm_wait(2 * NI));
+        if (tb + 2 * STEP < c1) __builtin_amdgcn_s_waitcnt(vm_wait(2 * NI));
+        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
         consume(wb1, tb + STEP);
         __builtin_amdgcn_s_waitcnt(kLgkm0);
-        issue(wb1, tb + 3 * STEP);
+        if (tb + 3 * STEP < c1) issue(wb1, tb + 3 * STEP);
     }
     __builtin_amdgcn_s_waitcnt(vm_wait(0));  // drain DMA before the LDS is reused
 
     l_part += __shfl_xor(l_part, 16, 64);
     l_part += __shfl_xor(l_part, 32, 64);
     __syncthreads();
-    float *sm = (float *)lds0;  // kMW*16*(D+2) floats fit in one stage array
-    float *sm_m = sm, *sm_l = sm + kMW * 16, *sm_o = sm + 2 * kMW * 16;
+    float *sm = (float *)lds0;  // MW*16*(D+2) floats fit in one stage array
+    float *sm_m = sm, *sm_l = sm + MW * 16, *sm_o = sm + 2 * MW * 16;
     if (kg == 0) { sm_m[wave * 16 + n16] = m_run; sm_l[wave * 16 + n16] = l_part; }
+    // Row pitch D + 4 floats: the 16 heads of a lane group land on different
+    // banks (a pitch of D would put them all on one).
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) sm_o[(wave * 16 + n16) * D + dt * 16 + kg * 4 + i] = oacc[dt][i];
+        *(f32x4 *)&sm_o[(wave * 16 + n16) * (D + 4) + dt * 16 + kg * 4] = oacc[dt];
     __syncthreads();
-    const int64_t u = (int64_t)b * n_units + unit;
-    const int GD = gt * D;
-    for (int idx = tid; idx < GD; idx += kMW * 64) {
-        const int g = idx / D, d = idx % D;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kMW; w++) mx = fmaxf(mx, sm_m[w * 16 + g]);
-        const float mu = mx == -INFINITY ? 0.f : mx;
-        float num = 0.f, den = 0.f;
-#pragma unroll
-        for (int w = 0; w < kMW; w++) {
-            const float c = exp2f(sm_m[w * 16 + g] - mu);
-            num += sm_o[(w * 16 + g) * D + d] * c;
-            den += sm_l[w * 16 + g] * c;
-        }
-        if (splits == 1) {
-            out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
-        } else {
-            ws_acc[(u * splits + split) * GD + idx] = num;
-            if (d == 0) {
-                ws_ml[((u * splits + split) * gt + g) * 2] = mx;
-                ws_ml[((u * splits + split) * gt + g) * 2 + 1] = den;
-            }
-        }
-    }
+    finish_unit<D, MW>(sm_m, sm_l, sm_o, b, unit, split, splits, gt, n_units, n_head, head0,
+                       out, ws_ml, ws_acc);
 }
 
 constexpr int kMaxSplits = 128;
@@ -544,19 +538,20 @@ constexpr int kMaxSplits = 128;
 // every load (the split rows of this thread's column group, then this
 // thread's split m/l) is issued branch-free (indices clamped, weights of
 // clamped duplicates zeroed) before any is consumed; then the log-sum-exp
-// weights are applied and the R split residues summed through LDS.
-// NL = partial rows per thread, ceil(splits / R).
+// weights are applied and the R split residues summed through LDS.  A
+// workgroup of kMergeThreads keeps many rows in flight per CU (the merge is
+// latency-bound on few CUs).  NL = partial rows per thread, ceil(splits / R).
+constexpr int kMergeThreads = 1024;
 template <int D, int NL>
-__global__ __launch_bounds__(256) void decode_merge_kernel(const float *__restrict__ ws_ml,
-                                                           const float *__restrict__ ws_acc,
-                                                           int splits, int gt, int n_units,
-                                                           int n_head, float *__restrict__ out) {
-    constexpr int NC = D / 4, R = 256 / NC;
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
+    const float *__restrict__ ws_ml, const float *__restrict__ ws_acc, int splits, int gt,
+    int n_units, int n_head, float *__restrict__ out) {
+    constexpr int NC = D / 4, R = kMergeThreads / NC;
     const int g = blockIdx.x, unit = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, col = tid % NC, r = tid / NC;
+    const int tid = threadIdx.x, col = tid % NC, r = tid / NC, lane = tid & 63;
     const int64_t u = (int64_t)b * n_units + unit;
     const int GD = gt * D;
-    __shared__ float sm_m[kMaxSplits], sm_l[kMaxSplits];
+    __shared__ float sm_m[kMaxSplits], sm_l[kMaxSplits], sm_w[kMaxSplits];
     __shared__ f32x4 red[R][NC];
     const float *accp = ws_acc + u * splits * GD + g * D + col * 4;
     f32x4 v[NL];
@@ -568,26 +563,35 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float *__restri
     const float lv = ws_ml[((u * splits + spm) * gt + g) * 2 + 1];
     if (tid < splits) { sm_m[tid] = mv; sm_l[tid] = lv; }
     __syncthreads();
+    // max over splits, one redundant reduction per wave
     float mx = -INFINITY;
-    for (int sp = 0; sp < splits; sp++) mx = fmaxf(mx, sm_m[sp]);
+    for (int sp = lane; sp < splits; sp += 64) mx = fmaxf(mx, sm_m[sp]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     const float mu = mx == -INFINITY ? 0.f : mx;
+    if (tid < splits) sm_w[tid] = __builtin_amdgcn_exp2f(sm_m[tid] - mu);
+    __syncthreads();
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NL; i++) {
         const int sp = r + i * R;
-        const float w = sp < splits ? exp2f(sm_m[min(sp, splits - 1)] - mu) : 0.f;
+        const float w = sp < splits ? sm_w[sp] : 0.f;
         a += v[i] * w;
     }
     red[r][col] = a;
     __syncthreads();
-    if (tid < NC) {
-        f32x4 t = red[0][tid];
-#pragma unroll
-        for (int rr = 1; rr < R; rr++) t += red[rr][tid];
+    if (tid < 64) {  // wave 0: the denominator, then NC output columns
         float den = 0.f;
-        for (int sp = 0; sp < splits; sp++) den += sm_l[sp] * exp2f(sm_m[sp] - mu);
+        for (int sp = lane; sp < splits; sp += 64) den += sm_l[sp] * sm_w[sp];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o, 64);
         const float inv = den > 0.f ? 1.0f / den : 0.f;
-        *(f32x4 *)(out + ((int64_t)b * n_head + unit * gt + g) * D + tid * 4) = t * inv;
+        for (int c = lane; c < NC; c += 64) {
+            f32x4 t = red[0][c];
+#pragma unroll 8
+            for (int rr = 1; rr < R; rr++) t += red[rr][c];
+            *(f32x4 *)(out + ((int64_t)b * n_head + unit * gt + g) * D + c * 4) = t * inv;
+        }
     }
 }
 
@@ -596,7 +600,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float *__restri
 namespace ullm {
 
 struct MfmaPlan {
-    int gt, n_units, chunk, splits;
+    int gt, n_units, chunk, splits, mw;
     size_t off_ml, off_acc, bytes;
 };
 
@@ -609,9 +613,16 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     p.n_units = n_head / p.gt;
     const int visible = (window > 0 && max_len > window) ? window : max_len;
     const int units = batch * p.n_units;
-    const int tile = kMW * kTok;
+    // Waves per workgroup: a short context spreads its blocks one wave per
+    // workgroup over every CU (a CU's outstanding misses, not the waves,
+    // bound how fast it streams); a long one uses 4-wave workgroups.
+    const int blocks = (visible + kTok - 1) / kTok;
+    p.mw = (D <= 128 && (int64_t)units * blocks <= 1024) ? 1 : kMW;
+    if (const char *e = getenv("ULLM_HIP_DECODE_MW"))  // tuning override
+        if (D <= 128 && (atoi(e) == 1 || atoi(e) == kMW)) p.mw = atoi(e);
+    const int tile = p.mw * kTok;
     int splits = (visible + tile - 1) / tile;
-    const int want = (kMfmaTargetWG + units - 1) / units;
+    const int want = (kMfmaTargetWG * (p.mw == 1 ? 2 : 1) + units - 1) / units;
     if (splits > want) splits = want;
     const int cap = kMaxSplits;
     if (splits > cap) splits = cap;
@@ -641,14 +652,15 @@ size_t decode_mfma_workspace(int batch, int n_head, int n_kv_head, int D, int ma
 template <class T, int D, bool DMA = (D <= 128)>
 struct MainLaunch {
     template <class... A>
-    static void run(dim3 g, hipStream_t st, A... a) {
-        hipLaunchKernelGGL((decode_dma_kernel<T, D>), g, dim3(kMW * 64), 0, st, a...);
+    static void run(int mw, dim3 g, hipStream_t st, A... a) {
+        if (mw == 1) hipLaunchKernelGGL((decode_dma_kernel<T, D, 1>), g, dim3(64), 0, st, a...);
+        else hipLaunchKernelGGL((decode_dma_kernel<T, D, kMW>), g, dim3(kMW * 64), 0, st, a...);
     }
 };
 template <class T, int D>
 struct MainLaunch<T, D, false> {
     template <class... A>
-    static void run(dim3 g, hipStream_t st, A... a) {
+    static void run(int, dim3 g, hipStream_t st, A... a) {
         hipLaunchKernelGGL((decode_mfma_kernel<T, D>), g, dim3(kMW * 64), 0, st, a...);
     }
 };
@@ -657,22 +669,21 @@ template <class T, int D>
 static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const void *vc,
                         int64_t kvs, int64_t ss, const int32_t *lens, int win, int batch, int nh,
                         int kv_mul, float qs, float *out, char *ws, hipStream_t st) {
-    MainLaunch<T, D>::run(dim3(p.splits, p.n_units, batch), st, q, (const char *)kc,
+    MainLaunch<T, D>::run(p.mw, dim3(p.splits, p.n_units, batch), st, q, (const char *)kc,
                           (const char *)vc, kvs, ss, lens, win, nh, kv_mul, p.gt, p.n_units,
                           p.chunk, p.splits, qs, out, (float *)(ws + p.off_ml),
                           (float *)(ws + p.off_acc));
     if (p.splits > 1) {
-        constexpr int R = 256 / (D / 4);
+        constexpr int R = kMergeThreads / (D / 4);
         const int nl = (p.splits + R - 1) / R;
         const dim3 g(p.gt, p.n_units, batch);
         const float *ml = (const float *)(ws + p.off_ml), *ac = (const float *)(ws + p.off_acc);
-#define ULLM_MERGE(NL) hipLaunchKernelGGL((decode_merge_kernel<D, NL>), g, dim3(256), 0, st, ml, \
-                                          ac, p.splits, p.gt, p.n_units, nh, out)
-        if (nl <= 2) ULLM_MERGE(2);
+#define ULLM_MERGE(NL) hipLaunchKernelGGL((decode_merge_kernel<D, NL>), g, dim3(kMergeThreads), 0, \
+                                          st, ml, ac, p.splits, p.gt, p.n_units, nh, out)
+        if (nl <= 1) ULLM_MERGE(1);
+        else if (nl <= 2) ULLM_MERGE(2);
         else if (nl <= 4) ULLM_MERGE(4);
-        else if (nl <= 8) ULLM_MERGE(8);
-        else if (nl <= 16) ULLM_MERGE(16);
-        else ULLM_MERGE(32);
+        else ULLM_MERGE(8);
 #undef ULLM_MERGE
     }
 }
