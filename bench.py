@@ -263,14 +263,14 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["gbps_step"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("bytes_per_launch") if traffic else None,
-                     "kernel": "decode_dma_kernel<F16,128> + decode_merge_kernel<128> "
+                     "kernel": "decode_dma_kernel<F16,128,1> + decode_merge_kernel<128,4> "
                                "(one decode-attention op per layer)",
                      "algorithmic_bytes": d["layer_bytes"],
                      "us_per_launch": round(d["us_per_layer"], 3)},
         "roofline_prefill": {"bound": "mfma", "achieved": round(p["tflops"], 2),
                              "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(p["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
-                             "kernel": "prefill_kernel<BF16,128>"},
+                             "kernel": "prefill4_kernel<BF16,128>"},
     }
     if not args.no_cpu:
         cb = cpu_baseline_decode(12, 2, 128, 4096, 28)
