@@ -51,7 +51,8 @@ const char *ullm_hip_version(void);
 const char *ullm_hip_last_error(void);
 
 /* Bytes of device workspace ullm_hip_attn_decode needs for this shape.
- * max_len is the largest seq_len the call will see.  The workspace holds
+ * max_len is the largest seq_len the calls will see; a workspace sized for
+ * max_len serves every call whose own max_len is smaller.  The workspace holds
  * split-KV partials plus a counter area that must be ZERO before its first
  * use; every completed decode call leaves the counters at zero again, so
  * one hipMemset at allocation suffices.  One workspace serves one stream at

@@ -121,6 +121,16 @@ def test_workspace_reuse_back_to_back(dev):
     run_case(dev, "f16", 12, 2, 128, [2000], seed=14, workspace=ws)
 
 
+@pytest.mark.parametrize("dtype,H,Hk", [("f16", 12, 2), ("bf16", 32, 4)])
+def test_workspace_sized_for_n_ctx_serves_shorter_calls(dev, dtype, H, Hk):
+    """A workspace sized once for n_ctx must serve every call with a smaller
+    max_len (decode passes max_len = pos + 1 each step), even where a short
+    context plans more splits than a long one."""
+    ws = A.new_decode_workspace(1, H, Hk, 128, 8192)
+    for L in (600, 2048, 4096, 8192):
+        run_case(dev, dtype, H, Hk, 128, [L], seed=15, workspace=ws)
+
+
 def test_workspace_too_small_is_an_error(dev):
     q = torch.zeros(1, 12, 128, device=dev)
     k = torch.zeros(4096, 256, dtype=torch.float16, device=dev)

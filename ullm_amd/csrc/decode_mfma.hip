@@ -26,6 +26,7 @@
 //    through registers (decode_mfma_kernel).
 //  * The waves of a workgroup stream disjoint key blocks and combine through
 //    LDS; the splits of a unit are combined by decode_merge_kernel.
+#include <algorithm>
 #include <cstdlib>
 #include "common.hpp"
 #include "mfma_util.hpp"
@@ -616,13 +617,16 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     // Waves per workgroup: a short context spreads its blocks one wave per
     // workgroup over every CU (a CU's outstanding misses, not the waves,
     // bound how fast it streams); a long one uses 4-wave workgroups.
+    // A context of at most kMW * 4 blocks stays in one 4-wave workgroup per
+    // unit: no partials, no merge kernel.
     const int blocks = (visible + kTok - 1) / kTok;
-    p.mw = (D <= 128 && (int64_t)units * blocks <= 1024) ? 1 : kMW;
+    p.mw = (D <= 128 && blocks > kMW * 4 && (int64_t)units * blocks <= 1024) ? 1 : kMW;
     if (const char *e = getenv("ULLM_HIP_DECODE_MW"))  // tuning override
         if (D <= 128 && (atoi(e) == 1 || atoi(e) == kMW)) p.mw = atoi(e);
     const int tile = p.mw * kTok;
     int splits = (visible + tile - 1) / tile;
     const int want = (kMfmaTargetWG * (p.mw == 1 ? 2 : 1) + units - 1) / units;
+    if (blocks <= kMW * 4) splits = 1;
     if (splits > want) splits = want;
     const int cap = kMaxSplits;
     if (splits > cap) splits = cap;
@@ -643,9 +647,20 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     return p;
 }
 
+// Upper bound over every call with max_len' <= max_len (the planner's split
+// count is not monotonic in the length: short contexts use more, smaller
+// splits): every split holds at least one 32-key block, at most kMaxSplits
+// exist, and contexts of at most kMW * 4 blocks use one split.
 size_t decode_mfma_workspace(int batch, int n_head, int n_kv_head, int D, int max_len,
                              int window) {
-    return plan_mfma(batch, n_head, n_kv_head, D, max_len, window).bytes;
+    const MfmaPlan p = plan_mfma(batch, n_head, n_kv_head, D, max_len, window);
+    const int visible = (window > 0 && max_len > window) ? window : max_len;
+    const int blocks = (visible + kTok - 1) / kTok;
+    const int smax = blocks <= kMW * 4 ? 1 : std::min(kMaxSplits, blocks);  // as plan_mfma
+    if (smax <= 1) return 0;
+    const size_t units = (size_t)batch * p.n_units;
+    const size_t ml = (units * smax * p.gt * 2 * 4 + 255) / 256 * 256;
+    return ml + units * smax * p.gt * D * 4;
 }
 
 // head_dim <= 128 streams through LDS DMA; 256 keeps register staging.
