@@ -257,6 +257,23 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void prefill_kernel(
 // without a window they are g and NG-1-g, so every workgroup carries the same
 // causal work (no tail of short workgroups); with a window they are adjacent.
 // Each wave owns 32 query rows of one head.
+// 16-byte slot swizzle of key row r in an LDS K/V tile (slot p of row r
+// holds chunk p ^ kv_swz(r)).  Two read patterns must be conflict-free:
+//  * K operand, ds_read_b128: one pass is 16 lanes = 16 consecutive rows
+//    reading the same chunk, so kv_swz must be a bijection on 16 rows (on
+//    the rows sharing a bank line for D = 64);
+//  * V^T operand, ds_read_b64_tr_b16: one pass is 16 lanes = 4 consecutive
+//    rows x one aligned pair of chunks, so kv_swz(r) >> 1 must differ within
+//    every aligned group of 4 rows.
+// D = 128 (256-byte rows span all 64 banks): bits 1-2 <- r bits 0-1,
+// bit 0 <- r bit 2, bit 3 <- r bit 3.  D = 64 (two rows per bank line):
+// bits 1-2 <- r bits 1-2, bit 0 <- r bit 3.
+template <int D>
+__device__ __forceinline__ int kv_swz(int r) {
+    if constexpr (D == 128) return ((r & 3) << 1) | ((r >> 2) & 1) | (r & 8);
+    else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
+}
+
 template <int D>
 struct PF2 {
     static constexpr int NW = 8;
@@ -338,7 +355,7 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
 #pragma unroll
     for (int i = 0; i < NIW; i++) {
         const int r = (wave * NIW + i) * RPI + lane / SLOTS;
-        dofs[i] = r * rbg + (((lane % SLOTS) ^ (r & (SLOTS - 1))) * 16);
+        dofs[i] = r * rbg + (((lane % SLOTS) ^ kv_swz<D>(r)) * 16);
     }
     const int kt0 = hi > 0 ? (max(lo, 0) / BN) : 0;
     const int nt = hi > 0 ? (hi + BN - 1) / BN - kt0 : 0;
@@ -422,7 +439,7 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
             u32x4 ka[NKS];
 #pragma unroll
             for (int s = 0; s < NKS; s++)
-                ka[s] = lds_read_b128(kbase + r * RB + (((s * 2 + h2) ^ (r & (SLOTS - 1))) * 16));
+                ka[s] = lds_read_b128(kbase + r * RB + (((s * 2 + h2) ^ kv_swz<D>(r)) * 16));
             lds_wait_any();
 #pragma unroll
             for (int s = 0; s < NKS; s++) tie(ka[s]);
@@ -487,8 +504,8 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
                 for (int ks = 0; ks < 2; ks++) {
                     const int R0 = kt * 32 + ks * 16 + hh * 4 + (i16 >> 2);
                     const int R1 = R0 + 8;
-                    const u32x2 a0 = lds_read_tr16_b64(vbase + R0 * RB + ((chq ^ (R0 & (SLOTS - 1))) * 16) + boff);
-                    const u32x2 a1 = lds_read_tr16_b64(vbase + R1 * RB + ((chq ^ (R1 & (SLOTS - 1))) * 16) + boff);
+                    const u32x2 a0 = lds_read_tr16_b64(vbase + R0 * RB + ((chq ^ kv_swz<D>(R0)) * 16) + boff);
+                    const u32x2 a1 = lds_read_tr16_b64(vbase + R1 * RB + ((chq ^ kv_swz<D>(R1)) * 16) + boff);
                     va[kt][ks] = u32x4{a0[0], a0[1], a1[0], a1[1]};
                 }
             lds_wait_any();
@@ -569,11 +586,7 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     static_assert(D <= 128 && BN == 64, "v4 tiling");
     static_assert(2 * TILE + (NKT * 32) * RB <= 65535, "immediate offsets");
     static_assert(4 * 64 * NDT * 64 + 32 * OROW <= 2 * VREG, "epilogue staging");
-    // 16-byte slot swizzle of key row r.  A 256-byte row (D = 128) spans all
-    // 64 banks, so the four rows one 16-lane transpose read touches must land
-    // on different slot pairs: XOR with 2r, not r.  128-byte rows (D = 64)
-    // alternate bank halves and use r itself.
-    auto swz = [](int r) { return D == 128 ? (r << 1) & (SLOTS - 1) : r & (SLOTS - 1); };
+    auto swz = [](int r) { return kv_swz<D>(r); };
     __shared__ __attribute__((aligned(1024))) char lds[2 * VREG];
     __shared__ float hand_ml[4][32][2];
     __shared__ uint32_t set_bar[2];
@@ -890,7 +903,11 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
             }
             if (j + 1 < n_me) raise_max(m_next);
         }
-        __builtin_amdgcn_s_waitcnt(vm_wait(0));  // item j+2's K, j+1's V, Q and stores retired
+        // Item j+2's K, j+1's V and Q retired.  In the step that wrote block
+        // A's rows, its NDT*4 stores (issued last) may still drain: they are
+        // counted, in order, after the DMA.
+        if (set == 0 && gB >= 0 && j == TA - 1) __builtin_amdgcn_s_waitcnt(vm_wait(NDT * 4));
+        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
         tie_q();
         widen_own(j);
     };
