@@ -533,7 +533,7 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
                        out, ws_ml, ws_acc);
 }
 
-constexpr int kMaxSplits = 128;
+constexpr int kMaxSplits = 256;
 
 // Combines the split partials of one (sequence, head) in one round trip:
 // every load (the split rows of this thread's column group, then this
@@ -616,16 +616,19 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     const int units = batch * p.n_units;
     // Waves per workgroup: a short context spreads its blocks one wave per
     // workgroup over every CU (a CU's outstanding misses, not the waves,
-    // bound how fast it streams); a long one uses 4-wave workgroups.
+    // bound how fast it streams).
     // A context of at most kMW * 4 blocks stays in one 4-wave workgroup per
     // unit: no partials, no merge kernel.
+    // Long contexts use 2-wave workgroups, two per CU (64 KB of LDS stages
+    // each): measured ~5 % faster at 32K than one 4-wave workgroup per CU.
     const int blocks = (visible + kTok - 1) / kTok;
-    p.mw = (D <= 128 && blocks > kMW * 4 && (int64_t)units * blocks <= 1024) ? 1 : kMW;
+    if (D > 128 || blocks <= kMW * 4) p.mw = kMW;
+    else p.mw = (int64_t)units * blocks <= 1024 ? 1 : 2;
     if (const char *e = getenv("ULLM_HIP_DECODE_MW"))  // tuning override
-        if (D <= 128 && (atoi(e) == 1 || atoi(e) == kMW)) p.mw = atoi(e);
+        if (D <= 128 && (atoi(e) == 1 || atoi(e) == 2 || atoi(e) == kMW)) p.mw = atoi(e);
     const int tile = p.mw * kTok;
     int splits = (visible + tile - 1) / tile;
-    const int want = (kMfmaTargetWG * (p.mw == 1 ? 2 : 1) + units - 1) / units;
+    const int want = (kMfmaTargetWG * (p.mw == kMW ? 1 : 2) + units - 1) / units;
     if (blocks <= kMW * 4) splits = 1;
     if (splits > want) splits = want;
     const int cap = kMaxSplits;
@@ -669,6 +672,7 @@ struct MainLaunch {
     template <class... A>
     static void run(int mw, dim3 g, hipStream_t st, A... a) {
         if (mw == 1) hipLaunchKernelGGL((decode_dma_kernel<T, D, 1>), g, dim3(64), 0, st, a...);
+        else if (mw == 2) hipLaunchKernelGGL((decode_dma_kernel<T, D, 2>), g, dim3(128), 0, st, a...);
         else hipLaunchKernelGGL((decode_dma_kernel<T, D, kMW>), g, dim3(kMW * 64), 0, st, a...);
     }
 };
