@@ -116,7 +116,7 @@ __device__ __forceinline__ i32x4 raw_rsrc(const void *base, int bytes) {
 }
 __device__ __forceinline__ u32x4 buffer_load_b128_untracked(const i32x4 &rsrc, int voff) {
     u32x4 v;
-    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc));
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc) : "memory");
     return v;
 }
 
