@@ -537,12 +537,14 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Prefill v4 (head_dim <= 128, GQA groups of 4k heads, no binding window):
+// Prefill v4 (head_dim <= 128, no binding window; any GQA ratio):
 // split-K inside the workgroup so that both waves of every SIMD compute at
 // every step.
 //
-// A workgroup owns 4 heads of one kv head and the causal pair of 32-row
-// blocks A = g, B = NG-1-g (TA and TB key tiles).  Its TA+TB tile-units are
+// A workgroup owns hw heads of one kv head (hw = 4, 2 or 1, the largest that
+// divides the GQA ratio) and the causal pair of 32 * (4 / hw)-row blocks
+// A = g, B = NG-1-g (TA and TB key tiles); the 4 waves of a set cover the
+// hw heads x 4 / hw row groups of 32, all sharing each K/V tile.  Its TA+TB tile-units are
 // cut into two equal streams: set 0 (waves 0-3) runs A's tiles [0, TA) and
 // then B's tiles [TA, n0); set 1 (waves 4-7) runs B's tiles [n0, TB) and
 // [0, TA).  Every wave keeps (m, l, O) for the 32 query rows of one head.
@@ -573,7 +575,7 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
 template <class T, int D>
 __global__ __launch_bounds__(512) void prefill4_kernel(
     const uint16_t *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
-    int64_t kv_stride, int S, int start_pos, int n_head, int kv_mul, int ng, int np,
+    int64_t kv_stride, int S, int start_pos, int n_head, int kv_mul, int lhw, int ng, int np,
     float qscale, float *__restrict__ out) {
     using C = PF2<D>;
     constexpr int BN = C::BN, RB = C::RB, SLOTS = C::SLOTS, RPI = C::RPI, NIW = C::NIW;
@@ -581,8 +583,7 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     constexpr int NSTG = 4, VREG = NSTG * TILE;
     constexpr bool CVTV = __is_same(T, BF16);
     constexpr float kLazy = 8.0f;  // log2 headroom before the max is raised
-    constexpr int OROW = 4 * D * 4;  // staged output row: 4 heads of f32
-    constexpr int CPR = OROW / 16;    // its 16-byte chunks, stored at chunk ^ (row & 15)
+    constexpr int OROW = 4 * D * 4;  // bytes of staged output per 32-row group (4 heads of f32)
     static_assert(D <= 128 && BN == 64, "v4 tiling");
     static_assert(2 * TILE + (NKT * 32) * RB <= 65535, "immediate offsets");
     static_assert(4 * 64 * NDT * 64 + 32 * OROW <= 2 * VREG, "epilogue staging");
@@ -591,14 +592,18 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     __shared__ float hand_ml[4][32][2];
     __shared__ uint32_t set_bar[2];
 
-    const int n_units = (n_head / kv_mul) * (kv_mul / 4);
+    // A set's 4 waves cover hw heads x rw row groups of 32 (hw * rw = 4): a
+    // "block" is 32 rw query rows of hw heads sharing one kv head.
+    const int hw = 1 << lhw, rw = 4 >> lhw, BLK = 32 * rw;
+    const int upk = kv_mul >> lhw;  // units per kv head
+    const int n_units = (n_head / kv_mul) * upk;
     const int total = n_units * np;
     const int per_xcd = (total + 7) / 8;
     const int tsk = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (tsk >= total) return;
     const int unit = tsk / np, pair = tsk % np;
-    const int kvh = unit / (kv_mul / 4);
-    const int head0 = kvh * kv_mul + (unit % (kv_mul / 4)) * 4;
+    const int kvh = unit / upk;
+    const int head0 = kvh * kv_mul + (unit % upk) * hw;
     const int gA = pair, gB = ng - 1 - pair != pair ? ng - 1 - pair : -1;
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -607,12 +612,13 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     const int c32 = lane & 31, h2 = lane >> 5;
     const int kv_len = start_pos + S;
     const int64_t q_dim = (int64_t)n_head * D;
-    const int head = head0 + slot;
+    const int head = head0 + (slot & (hw - 1));
+    const int sub = (slot >> lhw) * 32;  // this wave's row offset inside the block
 
     // ---- the two tile streams ----
-    const int rowA = gA * 32, rowB = gB >= 0 ? gB * 32 : rowA;  // rowB: merged block
-    const int TA = (start_pos + min(rowA + 32, S) + BN - 1) / BN;
-    const int TB = gB >= 0 ? (start_pos + min(rowB + 32, S) + BN - 1) / BN : 0;
+    const int rowA = gA * BLK, rowB = gB >= 0 ? gB * BLK : rowA;  // rowB: merged block
+    const int TA = (start_pos + min(rowA + BLK, S) + BN - 1) / BN;
+    const int TB = gB >= 0 ? (start_pos + min(rowB + BLK, S) + BN - 1) / BN : 0;
     const int n_tot = TA + TB;
     const int n0 = (n_tot + 1) / 2, n1 = n_tot - n0;
     // item i of stream s -> key tile, and whether it belongs to block A
@@ -706,7 +712,7 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     const i32x4 qrs = raw_rsrc(q, (int)((int64_t)S * q_dim * 2));
     u32x4 qv[NKS];
     auto load_q = [&](int row) {
-        const int o = (int)((min(row + c32, S) * q_dim + (int64_t)head * D + h2 * 8) * 2);
+        const int o = (int)((min(row + sub + c32, S) * q_dim + (int64_t)head * D + h2 * 8) * 2);
 #pragma unroll
         for (int s = 0; s < NKS; s++) qv[s] = buffer_load_b128_untracked(qrs, o + s * 32);
     };
@@ -755,8 +761,8 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     auto mask = [&](auto srcc, int row, int tile) {
         constexpr int SRC = decltype(srcc)::value;
         const int kb = tile * BN;
-        if (kb + BN - 1 > start_pos + row) {
-            const int pos_row = start_pos + row + c32;
+        if (kb + BN - 1 > start_pos + row + sub) {
+            const int pos_row = start_pos + row + sub + c32;
 #pragma unroll
             for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
@@ -884,7 +890,7 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
             if (set == 0 && gB >= 0 && j == TA - 1) {  // block A complete: write it, switch to B
                 const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
                 const float inv = 1.0f / l_tot;
-                const int qrow = rowA + c32;
+                const int qrow = rowA + sub + c32;
                 if (qrow < S) {
                     float *op = out + (int64_t)qrow * q_dim + (int64_t)head * D + h2 * 4;
 #pragma unroll
@@ -949,15 +955,16 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
 #pragma unroll
             for (int g = 0; g < 4; g++) o1[dt][g] = lds_read_b128(part + (dt * 4 + g) * 4 * 64 * 16);
         lds_wait_any();
-        const uint32_t dst = stg + c32 * OROW;
-        const int c0 = slot * (D / 4) + h2;
+        const int srow = sub + c32;  // staged row: hw heads x D f32
+        const uint32_t dst = stg + srow * (hw * D * 4);
+        const int c0 = (slot & (hw - 1)) * (D / 4) + h2;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++)
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 tie(o1[dt][g]);
                 const f32x4 b = __builtin_bit_cast(f32x4, o1[dt][g]);
-                lds_write_b128(dst + ((c0 + dt * 8 + g * 2) ^ (c32 & 15)) * 16,
+                lds_write_b128(dst + ((c0 + dt * 8 + g * 2) ^ (srow & 15)) * 16,
                                __builtin_bit_cast(u32x4, f32x4{oacc[dt][g * 4] * w0 + b[0] * w1,
                                                                oacc[dt][g * 4 + 1] * w0 + b[1] * w1,
                                                                oacc[dt][g * 4 + 2] * w0 + b[2] * w1,
@@ -966,14 +973,14 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     }
     __builtin_amdgcn_s_waitcnt(vm_wait(63) & ~(15 << 8));
     wg_barrier();
-    // 32 rows x (4 heads x D f32), contiguous in the output row: 8 waves x 4 rows.
-#pragma unroll
-    for (int r4 = 0; r4 < 4; r4++) {
-        const int r = wave * 4 + r4;
+    // BLK rows x (hw heads x D f32), contiguous in the output row: each wave
+    // stores BLK / 8 rows.
+    const int cpr = hw * D / 4;  // 16-byte chunks per staged row
+    for (int r4 = 0; r4 < rw * 4; r4++) {
+        const int r = wave * rw * 4 + r4;
         const int qrow = rowB + r;
-#pragma unroll
-        for (int c = lane; c < CPR; c += 64) {
-            const u32x4 v = lds_read_b128(stg + r * OROW + (c ^ (r & 15)) * 16);
+        for (int c = lane; c < cpr; c += 64) {
+            const u32x4 v = lds_read_b128(stg + r * (hw * D * 4) + (c ^ (r & 15)) * 16);
             lds_wait_any();
             if (qrow < S)
                 __builtin_nontemporal_store(__builtin_bit_cast(f32x4, v),
@@ -1017,10 +1024,11 @@ void PrefillLaunch<T, D, true>::run(const void *q, const void *kc, const void *v
     const int paired = !(win > 0 && win < sp + S);
     const int total = n_units * np;
     const int per_xcd = (total + 7) / 8;
-    if (D <= 128 && kv_mul % 4 == 0 && paired) {
+    if (D <= 128 && paired) {
+        const int lhw = hw == 4 ? 2 : (hw == 2 ? 1 : 0);
         hipLaunchKernelGGL((prefill4_kernel<T, D>), dim3(per_xcd * 8), dim3(512), 0, st,
                            (const uint16_t *)q, (const char *)kc, (const char *)vc, kvs, S, sp,
-                           nh, kv_mul, ng, np, qs, out);
+                           nh, kv_mul, lhw, ng, np, qs, out);
         return;
     }
     hipLaunchKernelGGL((prefill2_kernel<T, D>), dim3(per_xcd * 8), dim3(512), 0, st,
