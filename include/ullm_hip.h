@@ -74,7 +74,9 @@ size_t ullm_hip_decode_workspace_bytes(int batch, int n_head, int n_kv_head, int
  * v_cache:  layer base of sequence 0; sequence b starts seq_stride elements
  *           after sequence b-1 (ignored when batch == 1)
  * seq_lens: DEVICE int32[batch], each in 1..max_len
- * max_len:  host-side upper bound of seq_lens (sizes the split-KV grid)
+ * max_len:  host-side upper bound of seq_lens (sizes the split-KV grid);
+ *           keys 0..max_len-1 of every sequence must be readable memory
+ *           (keys from seq_lens[b] on may be fetched, never used)
  * out:      [batch][n_head][head_dim] f32
  * head_dim in {64, 128, 256}; n_head % n_kv_head == 0. */
 int ullm_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype,

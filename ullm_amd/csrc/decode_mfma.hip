@@ -39,41 +39,57 @@ constexpr int kTok = 32;        // keys per wave iteration (two 16-key tiles)
 constexpr int kMaxUnitHeads = 16;
 constexpr int kMfmaTargetWG = 256;  // one 4-wave workgroup per CU (LDS-bound)
 
+// Writes four columns (c*4 .. c*4+3) of head head0 + g for one split: the
+// normalised output when the unit has one split, else the partial (O
+// unnormalised; (m, l) once per head, by the thread of column group 0).
+template <int D>
+__device__ __forceinline__ void store_split(const f32x4 &num, float mx, float den, int c, int g,
+                                            int b, int split, int splits, int gt, int n_head,
+                                            int head0, int64_t u, int GD,
+                                            float *__restrict__ out, float *__restrict__ ws_ml,
+                                            float *__restrict__ ws_acc) {
+    if (splits == 1) {
+        f32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = den > 0.f ? num[i] / den : 0.f;
+        *(f32x4 *)(out + ((int64_t)b * n_head + head0 + g) * D + c * 4) = o;
+    } else {
+        *(f32x4 *)(ws_acc + (u * splits + split) * GD + g * D + c * 4) = num;
+        if (c == 0)
+            *(float2 *)(ws_ml + ((u * splits + split) * gt + g) * 2) = float2{mx, den};
+    }
+}
+
 // Finishes one (sequence, unit) split after its waves have staged their
 // (m, l, O) in LDS (sm_m, sm_l: [MW][16]; sm_o: [MW][16][D + 4]): combines
-// the waves; with one split writes `out`, otherwise writes the split's
-// partial (O unnormalised, m, l) for decode_merge_kernel.
+// the waves, four columns per thread; with one split writes `out`, otherwise
+// writes the split's partial (O unnormalised, then m, l) for
+// decode_merge_kernel.
 template <int D, int MW = kMW>
 __device__ void finish_unit(const float *sm_m, const float *sm_l, const float *sm_o, int b,
                             int unit, int split, int splits, int gt, int n_units, int n_head,
                             int head0, float *__restrict__ out, float *__restrict__ ws_ml,
                             float *__restrict__ ws_acc) {
-    constexpr int NT = MW * 64;
+    constexpr int NT = MW * 64, C4 = D / 4;
     const int tid = threadIdx.x;
     const int64_t u = (int64_t)b * n_units + unit;
     const int GD = gt * D;
-    for (int idx = tid; idx < GD; idx += NT) {
-        const int g = idx / D, d = idx % D;
+    for (int idx = tid; idx < gt * C4; idx += NT) {
+        const int g = idx / C4, c = idx % C4;
         float mx = -INFINITY;
 #pragma unroll
         for (int w = 0; w < MW; w++) mx = fmaxf(mx, sm_m[w * 16 + g]);
         const float mu = mx == -INFINITY ? 0.f : mx;
-        float num = 0.f, den = 0.f;
+        f32x4 num = {0.f, 0.f, 0.f, 0.f};
+        float den = 0.f;
 #pragma unroll
         for (int w = 0; w < MW; w++) {
-            const float c = __builtin_amdgcn_exp2f(sm_m[w * 16 + g] - mu);
-            num += sm_o[(w * 16 + g) * (D + 4) + d] * c;
-            den += sm_l[w * 16 + g] * c;
+            const float cw = __builtin_amdgcn_exp2f(sm_m[w * 16 + g] - mu);
+            num += *(const f32x4 *)&sm_o[(w * 16 + g) * (D + 4) + c * 4] * cw;
+            den += sm_l[w * 16 + g] * cw;
         }
-        if (splits == 1) {
-            out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
-        } else {
-            ws_acc[(u * splits + split) * GD + idx] = num;
-            if (d == 0) {
-                ws_ml[((u * splits + split) * gt + g) * 2] = mx;
-                ws_ml[((u * splits + split) * gt + g) * 2 + 1] = den;
-            }
-        }
+        store_split<D>(num, mx, den, c, g, b, split, splits, gt, n_head, head0, u, GD, out,
+                       ws_ml, ws_acc);
     }
 }
 
@@ -81,7 +97,7 @@ template <class T, int D>
 __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
-    int n_head, int kv_mul, int gt, int n_units, int chunk, int splits, float qscale,
+    int fetch_len, int n_head, int kv_mul, int gt, int n_units, int chunk, int splits, float qscale,
     float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc) {
     constexpr int NS = D / 32;      // QK k-steps (32 d each)
     constexpr int NDT = D / 16;     // 16-wide d tiles of O^T
@@ -108,10 +124,14 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
         }
     }
 
+    // fetch_len > 0: the window cannot bind and keys 0..fetch_len-1 are
+    // readable, so the first block is fetched before seq_lens[b] arrives
+    // (keys past the length are masked (K) and zeroed (V) once it is known).
     const int len = __builtin_amdgcn_readfirstlane(seq_lens[b]);
-    const int start = (window > 0 && len > window) ? len - window : 0;
-    const int c0 = start + split * chunk;
+    const int start = (fetch_len > 0 || window <= 0 || len <= window) ? 0 : len - window;
+    const int c0 = (fetch_len > 0 ? 0 : start) + split * chunk;
     const int c1 = min(c0 + chunk, len);
+    const int cf = fetch_len > 0 ? min(c0 + chunk, fetch_len) : c1;
 
     __shared__ __attribute__((aligned(16))) uint16_t vt_all[kMW][kTok * VP];
     uint16_t *vt = vt_all[wave];
@@ -127,7 +147,7 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     // of keys >= c1 fall outside the range and return zero.
     const char *kb0 = kc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
     const char *vb0 = vc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
-    const int range = c1 > 0 ? (c1 - 1) * rb + D * 2 : 0;
+    const int range = cf > 0 ? (cf - 1) * rb + D * 2 : 0;
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kb0), 0, range, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t vrs =
@@ -177,10 +197,14 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
                 sacc[t] = mfma16<T>(T_.k[t][s], ql[s], sacc[t]);
             }
         }
-        // V rows into the wave's LDS tile (row-major, padded pitch)
+        // V rows into the wave's LDS tile (row-major, padded pitch); fetched
+        // rows at or past the length are zeroed (P is 0 there, 0 * NaN is not)
 #pragma unroll
-        for (int i = 0; i < VL; i++)
-            *(u32x4 *)(vt + (vrow0 + i * KPI) * VP + vcol * 8) = T_.v[i];
+        for (int i = 0; i < VL; i++) {
+            u32x4 vv = T_.v[i];
+            if (fetch_len > 0 && tb + vrow0 + i * KPI >= c1) vv = u32x4{0u, 0u, 0u, 0u};
+            *(u32x4 *)(vt + (vrow0 + i * KPI) * VP + vcol * 8) = vv;
+        }
         // online softmax: lane = head n16, keys kg*4+i (tile 0) and 16+kg*4+i
         float sv[8];
 #pragma unroll
@@ -321,7 +345,7 @@ template <class T, int D, int MW>
 __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
-    int n_head, int kv_mul, int gt, int n_units, int chunk, int splits, float qscale,
+    int fetch_len, int n_head, int kv_mul, int gt, int n_units, int chunk, int splits, float qscale,
     float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc) {
     constexpr int NS = D / 32;          // QK k-steps (32 d each)
     constexpr int NDT = D / 16;         // 16-wide d tiles of O^T
@@ -349,15 +373,31 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
     char *const wb0 = lds0 + wave * STAGE;
     char *const wb1 = lds1 + wave * STAGE;
 
-    const int len = __builtin_amdgcn_readfirstlane(seq_lens[b]);
-    const int start = (window > 0 && len > window) ? len - window : 0;
-    const int c0 = start + split * chunk;
-    const int c1 = min(c0 + chunk, len);
+    // With fetch_len > 0 the window cannot bind (the split starts at
+    // split * chunk whatever the length) and keys 0..fetch_len-1 are
+    // readable: the K/V stream starts before seq_lens[b] arrives, over keys
+    // c0..cf-1, and keys past the length are masked (K) and zeroed (V) once
+    // it is known.  Otherwise the stream ends at the length (c1) and the
+    // buffer range returns zero past it.
+    // The length comes by a vector load (a scalar one would be waited for
+    // together with the kernel arguments, before anything is issued).
+    const __amdgpu_buffer_rsrc_t lrs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(seq_lens + b), 0, 4, kRsrcWord3);
+    int lenv = __builtin_amdgcn_raw_buffer_load_b32(lrs, 0, 0, 0);
+    int len, c1;
+    auto take_len = [&] {
+        asm volatile("" : "+v"(lenv));  // keeps the wait for it here
+        len = __builtin_amdgcn_readfirstlane(lenv);
+    };
+    if (fetch_len <= 0) take_len();
+    const int start = (fetch_len > 0 || window <= 0 || len <= window) ? 0 : len - window;
+    const int c0 = (fetch_len > 0 ? 0 : start) + split * chunk;
+    const int cf = fetch_len > 0 ? min(c0 + chunk, fetch_len) : min(c0 + chunk, len);
 
     const int rb = (int)(kv_stride * 2);
     const char *kb0 = kc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
     const char *vb0 = vc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
-    const int range = c1 > 0 ? (c1 - 1) * rb + D * 2 : 0;
+    const int range = cf > 0 ? (cf - 1) * rb + D * 2 : 0;
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kb0), 0, range, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t vrs =
@@ -392,12 +432,15 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
             qa[s][1] = *(const f32x4 *)(qp + (s * 4 + kg) * 8 + 4);
         }
     }
-    // Stages are issued only for keys that exist (a wave with one block
-    // issues one stage); the waits below count exactly what was issued.
+    // Stages are issued only for keys in the fetched range (a wave with one
+    // block issues one stage); a stage is waited for with the other stage
+    // still counted only when that one was issued, else with vmcnt(0).
     constexpr int STEP = MW * kTok;
     const int tb0 = c0 + wave * kTok;
-    if (tb0 < c1) issue(wb0, tb0);
-    if (tb0 + STEP < c1) issue(wb1, tb0 + STEP);
+    if (tb0 < cf) issue(wb0, tb0);
+    if (tb0 + STEP < cf) issue(wb1, tb0 + STEP);
+    if (fetch_len > 0) take_len();
+    c1 = min(c0 + chunk, len);
 
     u32x4 qh[NS], ql[NS];
 #pragma unroll
@@ -478,6 +521,14 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
                 ph[j] = pack2<T>(p[2 * j], p[2 * j + 1]);
             }
         }
+        if (fetch_len > 0 && tb + kTok > c1) {
+            // Fetched rows at or past the length hold whatever the cache
+            // holds there (P is 0 for them, but 0 * NaN is NaN): zero them.
+            const uint32_t vz = lds_addr(vt);
+            const int nv = max(c1 - tb, 0);
+            for (int i = nv * SLOTS + lane; i < kTok * SLOTS; i += 64)
+                lds_write_b128(vz + i * 16, u32x4{0u, 0u, 0u, 0u});
+        }
         // O^T += V^T . P^T; lane n16 of key group kg reads V rows kg*4 + n16/4
         // (+16), elements dt*16 + 4*(n16 % 4) .. +3, transposed by the read.
         const int vr0 = kg * 4 + (n16 >> 2);
@@ -502,8 +553,11 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
     // Unrolled by the two stages; each stage is refilled once its LDS reads
     // have retired (lgkmcnt(0)), two blocks ahead.
     constexpr int kLgkm0 = vm_wait(63) & ~(15 << 8);
+    // Past the first two stages only keys below the length are fetched, so
+    // from there on "issued" is "below c1".
     for (int tb = tb0; tb < c1; tb += 2 * STEP) {
-        if (tb + STEP < c1) __builtin_amdgcn_s_waitcnt(vm_wait(2 * NI));  // stage 1 in flight
+        const bool next1 = tb == tb0 ? tb + STEP < cf : tb + STEP < c1;
+        if (next1) __builtin_amdgcn_s_waitcnt(vm_wait(2 * NI));  // stage 1 in flight
         else __builtin_amdgcn_s_waitcnt(vm_wait(0));
         consume(wb0, tb);
         __builtin_amdgcn_s_waitcnt(kLgkm0);
@@ -519,6 +573,18 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
 
     l_part += __shfl_xor(l_part, 16, 64);
     l_part += __shfl_xor(l_part, 32, 64);
+    if constexpr (MW == 1) {
+        // One wave: its registers are the split's result (lane: head n16,
+        // columns dt*16 + kg*4 .. +3), written without an LDS round trip.
+        if (head_ok) {
+            const int64_t u = (int64_t)b * n_units + unit;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+                store_split<D>(oacc[dt], m_run, l_part, dt * 4 + kg, n16, b, split, splits, gt,
+                               n_head, head0, u, gt * D, out, ws_ml, ws_acc);
+        }
+        return;
+    }
     __syncthreads();
     float *sm = (float *)lds0;  // MW*16*(D+2) floats fit in one stage array
     float *sm_m = sm, *sm_l = sm + MW * 16, *sm_o = sm + 2 * MW * 16;
@@ -686,10 +752,15 @@ struct MainLaunch<T, D, false> {
 
 template <class T, int D>
 static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const void *vc,
-                        int64_t kvs, int64_t ss, const int32_t *lens, int win, int batch, int nh,
-                        int kv_mul, float qs, float *out, char *ws, hipStream_t st) {
+                        int64_t kvs, int64_t ss, const int32_t *lens, int max_len, int win,
+                        int batch, int nh, int kv_mul, float qs, float *out, char *ws,
+                        hipStream_t st) {
+    // Keys 0..max_len-1 of every sequence are readable (the cache holds them);
+    // when the window cannot bind, the kernels fetch keys before the length.
+    const int fetch_len = (win <= 0 || max_len <= win) ? max_len : 0;
     MainLaunch<T, D>::run(p.mw, dim3(p.splits, p.n_units, batch), st, q, (const char *)kc,
-                          (const char *)vc, kvs, ss, lens, win, nh, kv_mul, p.gt, p.n_units,
+                          (const char *)vc, kvs, ss, lens, win, fetch_len, nh, kv_mul, p.gt,
+                          p.n_units,
                           p.chunk, p.splits, qs, out, (float *)(ws + p.off_ml),
                           (float *)(ws + p.off_acc));
     if (p.splits > 1) {
@@ -718,7 +789,8 @@ int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64
     const int kv_mul = nh / nkv;
     char *w = (char *)ws;
 #define ULLM_MFMA_CASE(TT, DD) \
-    launch_mfma<TT, DD>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, w, st)
+    launch_mfma<TT, DD>(p, q, kc, vc, kvs, ss, lens, max_len, win, batch, nh, kv_mul, qs, \
+                        out, w, st)
     if (dtype == ULLM_DT_F16) {
         if (D == 64) ULLM_MFMA_CASE(F16, 64);
         else if (D == 128) ULLM_MFMA_CASE(F16, 128);
