@@ -601,34 +601,39 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
 
 constexpr int kMaxSplits = 256;
 
-// Combines the split partials of one (sequence, head) in one round trip:
-// every load (the split rows of this thread's column group, then this
-// thread's split m/l) is issued branch-free (indices clamped, weights of
-// clamped duplicates zeroed) before any is consumed; then the log-sum-exp
-// weights are applied and the R split residues summed through LDS.  A
-// workgroup of kMergeThreads keeps many rows in flight per CU (the merge is
-// latency-bound on few CUs).  NL = partial rows per thread, ceil(splits / R).
-constexpr int kMergeThreads = 1024;
+// Combines the split partials of one (sequence, head) in one round trip.
+// A workgroup takes D/4/kMergeGroups four-column groups of one head (the
+// merge of a few heads then still spreads over many CUs); every load (the
+// split rows of this thread's column group, then this thread's split m/l) is
+// issued branch-free (indices clamped, weights of clamped duplicates zeroed)
+// before any is consumed; then the log-sum-exp weights are applied and the R
+// split residues summed through LDS.  NL = partial rows per thread,
+// ceil(splits / R).
+constexpr int kMergeThreads = 256;
+constexpr int kMergeGroups = 4;
 template <int D, int NL>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     const float *__restrict__ ws_ml, const float *__restrict__ ws_acc, int splits, int gt,
     int n_units, int n_head, float *__restrict__ out) {
-    constexpr int NC = D / 4, R = kMergeThreads / NC;
-    const int g = blockIdx.x, unit = blockIdx.y, b = blockIdx.z;
+    constexpr int NC = D / 4 / kMergeGroups, R = kMergeThreads / NC;
+    const int g = blockIdx.x / kMergeGroups, cg = blockIdx.x % kMergeGroups;
+    const int unit = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, col = tid % NC, r = tid / NC, lane = tid & 63;
     const int64_t u = (int64_t)b * n_units + unit;
     const int GD = gt * D;
     __shared__ float sm_m[kMaxSplits], sm_l[kMaxSplits], sm_w[kMaxSplits];
-    __shared__ f32x4 red[R][NC];
-    const float *accp = ws_acc + u * splits * GD + g * D + col * 4;
+    __shared__ f32x4 red[kMergeThreads / 64][NC];
+    const int c4 = cg * NC + col;  // four-column group within the head
+    const float *accp = ws_acc + u * splits * GD + g * D + c4 * 4;
     f32x4 v[NL];
 #pragma unroll
     for (int i = 0; i < NL; i++)
         v[i] = *(const f32x4 *)(accp + (int64_t)min(r + i * R, splits - 1) * GD);
-    const int spm = min(tid, splits - 1);
-    const float mv = ws_ml[((u * splits + spm) * gt + g) * 2];
-    const float lv = ws_ml[((u * splits + spm) * gt + g) * 2 + 1];
-    if (tid < splits) { sm_m[tid] = mv; sm_l[tid] = lv; }
+    for (int sp = tid; sp < splits; sp += kMergeThreads) {
+        const float2 ml = *(const float2 *)(ws_ml + ((u * splits + sp) * gt + g) * 2);
+        sm_m[sp] = ml.x;
+        sm_l[sp] = ml.y;
+    }
     __syncthreads();
     // max over splits, one redundant reduction per wave
     float mx = -INFINITY;
@@ -636,7 +641,8 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     const float mu = mx == -INFINITY ? 0.f : mx;
-    if (tid < splits) sm_w[tid] = __builtin_amdgcn_exp2f(sm_m[tid] - mu);
+    for (int sp = tid; sp < splits; sp += kMergeThreads)
+        sm_w[sp] = __builtin_amdgcn_exp2f(sm_m[sp] - mu);
     __syncthreads();
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -645,9 +651,15 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
         const float w = sp < splits ? sm_w[sp] : 0.f;
         a += v[i] * w;
     }
-    red[r][col] = a;
+    // Sum the split residues: across the lanes of a wave holding one column
+    // group (lane bits above the column), then across the waves.
+#pragma unroll
+    for (int o = NC; o < 64; o <<= 1)
+#pragma unroll
+        for (int i = 0; i < 4; i++) a[i] += __shfl_xor(a[i], o, 64);
+    if (lane < NC) red[tid >> 6][col] = a;
     __syncthreads();
-    if (tid < 64) {  // wave 0: the denominator, then NC output columns
+    if (tid < 64) {  // wave 0: the denominator, then the NC output columns
         float den = 0.f;
         for (int sp = lane; sp < splits; sp += 64) den += sm_l[sp] * sm_w[sp];
 #pragma unroll
@@ -655,9 +667,10 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
         const float inv = den > 0.f ? 1.0f / den : 0.f;
         for (int c = lane; c < NC; c += 64) {
             f32x4 t = red[0][c];
-#pragma unroll 8
-            for (int rr = 1; rr < R; rr++) t += red[rr][c];
-            *(f32x4 *)(out + ((int64_t)b * n_head + unit * gt + g) * D + c * 4) = t * inv;
+#pragma unroll
+            for (int w = 1; w < kMergeThreads / 64; w++) t += red[w][c];
+            *(f32x4 *)(out + ((int64_t)b * n_head + unit * gt + g) * D + (cg * NC + c) * 4) =
+                t * inv;
         }
     }
 }
@@ -764,16 +777,17 @@ static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const
                           p.chunk, p.splits, qs, out, (float *)(ws + p.off_ml),
                           (float *)(ws + p.off_acc));
     if (p.splits > 1) {
-        constexpr int R = kMergeThreads / (D / 4);
+        constexpr int R = kMergeThreads / (D / 4 / kMergeGroups);
         const int nl = (p.splits + R - 1) / R;
-        const dim3 g(p.gt, p.n_units, batch);
+        const dim3 g(p.gt * kMergeGroups, p.n_units, batch);
         const float *ml = (const float *)(ws + p.off_ml), *ac = (const float *)(ws + p.off_acc);
 #define ULLM_MERGE(NL) hipLaunchKernelGGL((decode_merge_kernel<D, NL>), g, dim3(kMergeThreads), 0, \
                                           st, ml, ac, p.splits, p.gt, p.n_units, nh, out)
         if (nl <= 1) ULLM_MERGE(1);
         else if (nl <= 2) ULLM_MERGE(2);
         else if (nl <= 4) ULLM_MERGE(4);
-        else ULLM_MERGE(8);
+        else if (nl <= 8) ULLM_MERGE(8);
+        else ULLM_MERGE(16);
 #undef ULLM_MERGE
     }
 }
