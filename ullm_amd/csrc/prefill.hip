@@ -7,243 +7,29 @@
 // of lib.rs:1183-1186 applied per row as the Metal kernel does
 // (shader.metal:1051).
 //
-// Design:
-//  * A workgroup is 4 waves and owns BM = 128 query rows of one head; each
-//    wave owns 32 rows.  Per iteration the workgroup stages BN keys of K
-//    (as stored) and V (transposed to [d][key] and widened to f16) in LDS.
-//  * S^T = K . Q^T runs on v_mfma_f32_32x32x16_{bf16,f16}: K tiles from LDS
-//    are the A operand, the wave's Q rows stay in registers as the B operand.
-//    In the S^T accumulator every lane holds ONE query row (lane % 32) and 16
-//    keys, so the row max needs a single cross-lane exchange (lane ^ 32) and
-//    the row sum stays lane-local until the end.
-//  * The same accumulator, exponentiated and rounded to f16, IS the B operand
-//    of O^T += V^T . P^T (v_mfma_f32_32x32x16_f16): the keys' order inside a
-//    k-step is free, so V^T is read from LDS in the accumulator's key order
-//    and no register shuffle of P is needed.  P.V in f16 keeps the rounding of
-//    P at 2^-11 (bf16 would cost 2^-8 relative, beyond a 1e-3 rel-L2 budget).
-//  * Online softmax in the exp2 domain (scale*log2(e) folded into one
-//    multiply), f32 statistics and accumulators.
-//  * Tiles are ordered kv-head major and, within a kv head, longest causal
-//    row block first; blocks are dealt to the 8 XCDs so that all query heads
-//    of one kv head share one XCD's L2 (workgroup i runs on XCD i % 8).
+// Three kernels, all with f32 softmax statistics and accumulators, the
+// online softmax in the exp2 domain (scale*log2(e) folded into one multiply),
+// QK^T on v_mfma_f32_32x32x16_{bf16,f16} and P.V on the f16 variant (P and a
+// bf16 V rounded to f16: 2^-11 relative, where bf16 P would cost 2^-8):
+//  * prefill4_kernel (head_dim <= 128, no binding window): 8-wave
+//    workgroups over a pair of causal row blocks, split-K between two
+//    4-wave sets, K/V tiles shared through an LDS ring filled by DMA;
+//  * prefill2_kernel (head_dim <= 128, binding sliding window): the same
+//    staging without the split;
+//  * prefill_sk_kernel (head_dim 256): one 32-row block of one head per
+//    workgroup, split-K over its 4 waves, merged through LDS.
+// In every kernel the S^T = K.Q^T accumulator holds ONE query row per lane
+// (lane % 32) and 16 keys, so the row max needs a single cross-lane exchange
+// (lane ^ 32); exponentiated and rounded to f16 it IS the B operand of
+// O^T += V^T.P^T (the keys' order inside a k-step is free, so V^T is read
+// from LDS in the accumulator's key order).  Work is dealt to the 8 XCDs so
+// that the query heads of one kv head share an XCD's L2 (workgroup i runs on
+// XCD i % 8).
 #include "common.hpp"
 #include "mfma_util.hpp"
 #include "wave.hpp"
 
 namespace ullm {
-
-template <int D>
-struct PrefillCfg {
-    static constexpr int BM = 128;                    // query rows per workgroup
-    static constexpr int BN = D <= 128 ? 64 : 32;     // keys per iteration
-    static constexpr int KP = D + 8;                  // K row pitch in LDS (elements)
-    static constexpr int VP = BN + 8;                 // V^T row pitch in LDS (elements)
-    static constexpr int CPR = D / 8;                 // 16-byte chunks per key row
-    static constexpr int NCH = BN * CPR / 256;        // chunks (rows) per thread per tile
-    static constexpr int NKT = BN / 32;               // 32-key MFMA tiles per iteration
-    static constexpr int NDT = D / 32;                // 32-wide d tiles of the output
-    static constexpr int NKS = D / 16;                // 16-deep k steps of Q.K
-    static_assert(NCH >= 1 && 256 % CPR == 0, "staging map");
-};
-
-template <class T>
-__device__ __forceinline__ f32x16 mfma_qk(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
-    if constexpr (sizeof(T) && T::bytes == 2 && __is_same(T, BF16))
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-    else
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-
-__device__ __forceinline__ uint32_t to_f16_pair(float lo, float hi) {
-    return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
-}
-
-template <class T, int D>
-__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void prefill_kernel(
-    const uint16_t *__restrict__ q, const uint16_t *__restrict__ kc,
-    const uint16_t *__restrict__ vc, int64_t kv_stride, int S, int start_pos, int window,
-    int n_head, int kv_mul, float qscale, float *__restrict__ out) {
-    using C = PrefillCfg<D>;
-    constexpr int BM = C::BM, BN = C::BN, KP = C::KP, VP = C::VP, CPR = C::CPR, NCH = C::NCH;
-    constexpr int NKT = C::NKT, NDT = C::NDT, NKS = C::NKS;
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[BN * KP];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VP];
-
-    // ---- tile assignment (XCD-aware, longest first) ----
-    const int nqb = (S + BM - 1) / BM;
-    const int total = n_head * nqb;
-    const int per_xcd = (total + 7) / 8;
-    const int t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (t >= total) return;
-    const int per_kvh = nqb * kv_mul;
-    const int kvh = t / per_kvh, r = t % per_kvh;
-    const int qb = nqb - 1 - r / kv_mul;
-    const int h = kvh * kv_mul + r % kv_mul;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c = lane & 31, h2 = lane >> 5;
-    const int q0 = qb * BM, qw = q0 + wave * 32;
-    const int64_t q_dim = (int64_t)n_head * D;
-    const int kv_len = start_pos + S;
-
-    // ---- Q rows of this wave as the B operand (d = s*16 + h2*8 + j) ----
-    const int qrow = qw + c;
-    const bool row_ok = qrow < S;
-    u32x4 qreg[NKS];
-    {
-        const uint16_t *qp = q + (int64_t)(row_ok ? qrow : 0) * q_dim + (int64_t)h * D + h2 * 8;
-#pragma unroll
-        for (int s = 0; s < NKS; s++) qreg[s] = row_ok ? ld16(qp + s * 16) : u32x4{0, 0, 0, 0};
-    }
-    const int pos_row = start_pos + qrow;
-
-    // ---- key range of the workgroup and of this wave ----
-    const int wg_last = start_pos + min(q0 + BM, S) - 1;  // largest position in the block
-    const int kv_hi = wg_last + 1;
-    int kv_lo = 0;
-    if (window > 0) kv_lo = max(0, start_pos + q0 + 1 - window);
-    kv_lo = (kv_lo / BN) * BN;
-    const int w_first = start_pos + qw;                   // smallest position of the wave
-    const int w_last = start_pos + min(qw + 32, S) - 1;   // largest (may be < w_first)
-
-    f32x16 oacc[NDT];
-#pragma unroll
-    for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
-    float m_run = -INFINITY, l_part = 0.f;
-
-    // ---- staging map: thread -> (column chunk cc, rows rg*NCH .. +NCH) ----
-    const int cc = tid % CPR, rg = tid / CPR;
-    const uint16_t *kg = kc + (int64_t)kvh * D + cc * 8;
-    const uint16_t *vg = vc + (int64_t)kvh * D + cc * 8;
-    u32x4 kpre[NCH], vpre[NCH];
-    auto prefetch = [&](int kb) {
-#pragma unroll
-        for (int i = 0; i < NCH; i++) {
-            const int key = kb + rg * NCH + i;
-            const bool ok = key < kv_len;
-            kpre[i] = ok ? ld16(kg + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};
-            vpre[i] = ok ? ld16(vg + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};
-        }
-    };
-    prefetch(kv_lo);
-
-    for (int kb = kv_lo; kb < kv_hi; kb += BN) {
-        __syncthreads();  // previous tile fully consumed
-#pragma unroll
-        for (int i = 0; i < NCH; i++)
-            *(u32x4 *)&Ks[(rg * NCH + i) * KP + cc * 8] = kpre[i];
-        // V^T: element (d = cc*8 + j, key = rg*NCH + i), widened to f16.
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            float vf[NCH];
-#pragma unroll
-            for (int i = 0; i < NCH; i++) {
-                const uint32_t w = vpre[i][j >> 1];
-                if constexpr (__is_same(T, BF16)) vf[i] = (j & 1) ? bf16_hi(w) : bf16_lo(w);
-                else vf[i] = (j & 1) ? f16_hi(w) : f16_lo(w);
-            }
-            uint16_t *dst = &Vt[(cc * 8 + j) * VP + rg * NCH];
-            if constexpr (NCH == 4) {
-                *(u32x2 *)dst = u32x2{to_f16_pair(vf[0], vf[1]), to_f16_pair(vf[2], vf[3])};
-            } else if constexpr (NCH == 2) {
-                *(uint32_t *)dst = to_f16_pair(vf[0], vf[1]);
-            } else {
-#pragma unroll
-                for (int i = 0; i < NCH; i++) dst[i] = f32_to_f16_bits(vf[i]);
-            }
-        }
-        __syncthreads();
-        if (kb + BN < kv_hi) prefetch(kb + BN);
-
-        // Skip the MFMA work when the whole tile is masked for this wave.
-        const bool causal_dead = kb > w_last;
-        const bool window_dead = window > 0 && kb + BN - 1 < w_first + 1 - window;
-        if (causal_dead || window_dead || qw >= S) continue;
-
-        // ---- S^T = K . Q^T ----
-        f32x16 sacc[NKT];
-#pragma unroll
-        for (int kt = 0; kt < NKT; kt++) {
-            sacc[kt] = f32x16{};
-            const uint16_t *kr = &Ks[(kt * 32 + c) * KP + h2 * 8];
-#pragma unroll
-            for (int s = 0; s < NKS; s++)
-                sacc[kt] = mfma_qk<T>(*(const u32x4 *)(kr + s * 16), qreg[s], sacc[kt]);
-        }
-
-        // ---- online softmax over this tile (lane = one query row) ----
-        const bool need_mask = (kb + BN - 1 > w_first) || (window > 0 && kb < w_last + 1 - window);
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < NKT; kt++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                float sv = sacc[kt][i] * qscale;
-                if (need_mask) {
-                    const int key = kb + kt * 32 + (i >> 2) * 8 + h2 * 4 + (i & 3);
-                    const bool dead = key > pos_row || (window > 0 && key <= pos_row - window);
-                    sv = dead ? -INFINITY : sv;
-                }
-                sacc[kt][i] = sv;
-                mloc = fmaxf(mloc, sv);
-            }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float m_new = fmaxf(m_run, mloc);
-        const float mu = m_new == -INFINITY ? 0.f : m_new;
-        const float corr = exp2f(m_run - mu);
-        m_run = m_new;
-        float psum = 0.f;
-        u32x4 pk[NKT][2];
-#pragma unroll
-        for (int kt = 0; kt < NKT; kt++)
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-                for (int jj = 0; jj < 4; jj++) {
-                    const float p0 = exp2f(sacc[kt][ks * 8 + 2 * jj] - mu);
-                    const float p1 = exp2f(sacc[kt][ks * 8 + 2 * jj + 1] - mu);
-                    psum += p0 + p1;
-                    pk[kt][ks][jj] = to_f16_pair(p0, p1);
-                }
-        l_part = l_part * corr + psum;
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) oacc[dt] *= corr;
-
-        // ---- O^T += V^T . P^T (keys in accumulator order) ----
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-            const uint16_t *vr = &Vt[(dt * 32 + c) * VP + h2 * 4];
-#pragma unroll
-            for (int kt = 0; kt < NKT; kt++)
-#pragma unroll
-                for (int ks = 0; ks < 2; ks++) {
-                    const int kofs = kt * 32 + ks * 16;
-                    const u32x2 lo = *(const u32x2 *)(vr + kofs);
-                    const u32x2 hi = *(const u32x2 *)(vr + kofs + 8);
-                    const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, pk[kt][ks]),
-                        oacc[dt], 0, 0, 0);
-                }
-        }
-    }
-
-    // ---- normalise and store: lane holds row qrow, d = dt*32 + g*8 + h2*4 + 0..3 ----
-    const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
-    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-    if (!row_ok) return;
-    float *op = out + (int64_t)qrow * q_dim + (int64_t)h * D + h2 * 4;
-#pragma unroll
-    for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            f32x4 v = {oacc[dt][g * 4] * inv, oacc[dt][g * 4 + 1] * inv, oacc[dt][g * 4 + 2] * inv,
-                       oacc[dt][g * 4 + 3] * inv};
-            *(f32x4 *)(op + dt * 32 + g * 8) = v;
-        }
-}
 
 // ---------------------------------------------------------------------------
 // Prefill v2: K/V tiles shared by 8 waves through a 3-stage LDS ring filled by
@@ -545,7 +331,7 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
 // divides the GQA ratio) and the causal pair of 32 * (4 / hw)-row blocks
 // A = g, B = NG-1-g (TA and TB key tiles); the 4 waves of a set cover the
 // hw heads x 4 / hw row groups of 32, all sharing each K/V tile.  Its TA+TB tile-units are
-// cut into two equal streams: set 0 (waves 0-3) runs A's tiles [0, TA) and
+// cut into two streams (set 0 slightly longer): set 0 (waves 0-3) runs A's tiles [0, TA) and
 // then B's tiles [TA, n0); set 1 (waves 4-7) runs B's tiles [n0, TB) and
 // [0, TA).  Every wave keeps (m, l, O) for the 32 query rows of one head.
 // A's output is written by set 0 as soon as its last tile is done; B's two
@@ -620,7 +406,12 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     const int TA = (start_pos + min(rowA + BLK, S) + BN - 1) / BN;
     const int TB = gB >= 0 ? (start_pos + min(rowB + BLK, S) + BN - 1) / BN : 0;
     const int n_tot = TA + TB;
-    const int n0 = (n_tot + 1) / 2, n1 = n_tot - n0;
+    // Set 0 takes 34/64 of the tiles: set 1's waves are younger and lose
+    // issue arbitration to set 0's, so its steps run ~15 % slower (measured
+    // 1-3 % faster overall than an even split).  n0 >= TA holds (TA <= TB)
+    // and n0 <= TB keeps set 1's first tile inside block B.
+    const int n0 = min((n_tot * 34 + 63) / 64, gB >= 0 ? TB : n_tot);
+    const int n1 = n_tot - n0;
     // item i of stream s -> key tile, and whether it belongs to block A
     // (only set 0 has A items when the block has a partner).
     auto item_tile = [&](int s_, int i) {
@@ -989,18 +780,298 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     }
 }
 
-// head_dim 256 keeps the register-staged kernel (the LDS-ring variant needs
-// more than the 256 registers two waves per SIMD allow).
+// ---------------------------------------------------------------------------
+// Prefill with split-K inside the workgroup (head_dim 256).
+//
+// A workgroup owns one 32-row block of one query head; its 4 waves split the
+// block's key tiles (32 keys each) into 4 contiguous ranges, each wave keeps
+// (m, l, O) of all 32 rows over its range, and the 4 partials are merged
+// through LDS at the end (the online softmax is order-free).  That makes
+// n_head * ceil(S / 32) workgroups: at S = 1024 with 8 heads, 256, one per CU,
+// where 128-row workgroups would leave three quarters of the CUs idle.  One
+// wave per SIMD: the D = 256 output (128 registers), Q (64) and a K tile (64)
+// exceed what two waves per SIMD may hold.
+// Per wave and tile, K goes global -> registers in the MFMA A-operand layout
+// (lane = key row, 16-byte chunks); tile t+1's K is requested as soon as
+// tile t's QK MFMAs have read theirs.  V goes global -> the wave's own LDS
+// stage by buffer_load ... lds (row-major, 16-byte chunks XOR-swizzled by row
+// as kv_swz<128> does, bf16 widened to f16 in place) and is read transposed
+// as the V^T operand; two stages, V of tile t+1 in flight while t computes.
+template <class T, int D>
+__global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
+    const uint16_t *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
+    int64_t kv_stride, int S, int start_pos, int window, int n_head, int kv_mul, int nb,
+    float qscale, float *__restrict__ out) {
+    constexpr int BN = 32, RB = D * 2, SLOTS = D / 8, RPI = 1024 / RB, NI = BN / RPI;
+    constexpr int TILE = BN * RB;  // bytes of one V tile
+    constexpr int NKS = D / 16, NDT = D / 32, CPW = D / 16;
+    constexpr bool CVTV = __is_same(T, BF16);
+    constexpr float kLazy = 8.0f;  // log2 headroom before the max is raised
+    static_assert(D == 256, "split-K prefill serves head_dim 256");
+    static_assert(32 * D * 4 <= 2 * TILE, "a wave's partial fits its two V stages");
+    auto swz = [](int r) { return kv_swz<128>(r); };  // 4-row groups and 16-row bijection
+    __shared__ __attribute__((aligned(1024))) char lds[4 * 2 * TILE];
+    __shared__ float sm_ml[4][32][2];
+
+    // Tasks are head-major (the heads of one kv head are adjacent and share
+    // an XCD's L2: workgroup i runs on XCD i % 8), longest block first.
+    const int total = n_head * nb;
+    const int per_xcd = (total + 7) / 8;
+    const int tsk = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (tsk >= total) return;
+    const int head = tsk / nb, blk = nb - 1 - tsk % nb;
+    const int kvh = head / kv_mul;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, h2 = lane >> 5;
+    const int q0 = blk * 32;
+    const int64_t q_dim = (int64_t)n_head * D;
+    const int kv_len = start_pos + S;
+
+    // Key tiles of the block, [lo, hi) in keys, split over the 4 waves.
+    const int hi = start_pos + min(q0 + 32, S);
+    int lo = 0;
+    if (window > 0) lo = max(0, start_pos + q0 + 1 - window);
+    lo = lo / BN * BN;
+    const int nt = (hi - lo + BN - 1) / BN;
+    const int ta = lo / BN + nt * wave / 4, tb = lo / BN + nt * (wave + 1) / 4;
+
+    // Q rows of this wave as the B operand (d = s*16 + h2*8 + j).
+    const int qrow = q0 + c;
+    const bool row_ok = qrow < S;
+    const int pos_row = start_pos + qrow;
+    u32x4 qreg[NKS];
+    {
+        const uint16_t *qp = q + (int64_t)(row_ok ? qrow : 0) * q_dim + (int64_t)head * D + h2 * 8;
+#pragma unroll
+        for (int s = 0; s < NKS; s++) qreg[s] = row_ok ? ld16(qp + s * 16) : u32x4{0, 0, 0, 0};
+    }
+
+    const int rbg = (int)(kv_stride * 2);
+    const int range = (kv_len - 1) * rbg + D * 2;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
+    char *const vst = lds + wave * 2 * TILE;  // this wave's two V stages
+    const int koff = c * rbg + h2 * 16;
+    const int lr = lane / SLOTS, slot = lane % SLOTS;
+    // Requests are issued unconditionally (fixed wait counts); a tile past
+    // this wave's range is addressed past the buffer range, which reads
+    // zero without touching memory, as do keys past the cache's end.
+    auto tile_off = [&](int t) { return __builtin_amdgcn_readfirstlane(t < tb ? t * BN * rbg : range); };
+    auto issue_k = [&](u32x4(&kr)[NKS], int t) {
+        const int so = tile_off(t);
+#pragma unroll
+        for (int s = 0; s < NKS; s++)
+            kr[s] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff + s * 32 + so, 0, 0));
+        __builtin_amdgcn_sched_barrier(0);  // keep the K loads ahead of later V requests
+    };
+    auto issue_v = [&](int st, int t) {
+        const int so = tile_off(t);
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int r = i * RPI + lr;
+            dma16(vrs, vst + st * TILE + i * 1024, r * rbg + ((slot ^ swz(r)) * 16) + so, 0);
+        }
+    };
+    // bf16 -> f16 in place, for the chunks this lane's DMA wrote.
+    auto widen = [&](int st) {
+        if constexpr (CVTV) {
+            const uint32_t vb = lds_addr(vst + st * TILE) + lane * 16;
+#pragma unroll
+            for (int i0 = 0; i0 < NI; i0 += 4) {
+                u32x4 w[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) w[i] = lds_read_b128(vb + (i0 + i) * 1024);
+                lds_wait_any();
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    tie(w[i]);
+                    u32x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) o[e] = pack_f16x2(bf16_lo(w[i][e]), bf16_hi(w[i][e]));
+                    lds_write_b128(vb + (i0 + i) * 1024, o);
+                }
+            }
+        }
+    };
+
+    // V^T operand addresses (stage 0, k-step 0): lane gets d = dt*32 + lane%32
+    // ... as the transposing read delivers it, keys in the P^T order.
+    const int g16 = lane >> 4, i16 = lane & 15;
+    uint32_t va_addr[NDT][2];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int e0 = dt * 32 + (g16 & 1) * 16 + 4 * (i16 & 3);
+            const int R = (g16 >> 1) * 4 + (i16 >> 2) + h * 8;
+            va_addr[dt][h] = lds_addr(vst) + R * RB + (((e0 >> 3) ^ swz(R)) * 16) + (e0 & 7) * 2;
+        }
+
+    f32x16 oacc[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
+    float m_run = -INFINITY, l_part = 0.f;
+
+    u32x4 kreg[NKS];
+    auto consume = [&](auto stc, int t) {
+        constexpr int SOFF = decltype(stc)::value * TILE;
+        // S^T = K . Q^T: lane = query row c, keys (i>>2)*8 + h2*4 + (i&3)
+        f32x16 sacc = f32x16{};
+#pragma unroll
+        for (int s = 0; s < NKS; s++) sacc = mfma32<T>(kreg[s], qreg[s], sacc);
+        issue_k(kreg, t + 1);  // the MFMAs above have read their K
+        const int kb = t * BN;
+        const bool need_mask = kb + BN - 1 > start_pos + q0 ||
+                               (window > 0 && kb <= start_pos + q0 + 31 - window);
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            float sv = sacc[i] * qscale;
+            if (need_mask) {
+                const int key = kb + (i >> 2) * 8 + h2 * 4 + (i & 3);
+                const bool dead = key > pos_row || (window > 0 && key <= pos_row - window);
+                sv = dead ? -INFINITY : sv;
+            }
+            sacc[i] = sv;
+            mloc = fmaxf(mloc, sv);
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        // Lazy max: raised only when a row's tile max passes it by 2^kLazy
+        // (P = exp2(s - m) <= 256 stays exact in f16's range), so the O
+        // rescale (128 accumulators) runs a few times per wave, not per tile.
+        if (__any(mloc > m_run + kLazy)) {
+            const float m_new = fmaxf(m_run, mloc);
+            if (__any(m_run != -INFINITY)) {
+                const float corr = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+                l_part *= corr;
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) oacc[dt] *= corr;
+            }
+            m_run = m_new;
+        }
+        const float mu = m_run == -INFINITY ? 0.f : m_run;
+        u32x4 pk[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const float p0 = __builtin_amdgcn_exp2f(sacc[ks * 8 + 2 * jj] - mu);
+                const float p1 = __builtin_amdgcn_exp2f(sacc[ks * 8 + 2 * jj + 1] - mu);
+                l_part += p0 + p1;
+                pk[ks][jj] = pack_f16x2(p0, p1);
+            }
+        // O^T += V^T . P^T, the V^T reads of d tile dt + 1 in flight during dt's MFMAs
+        u32x2 vb[2][2][2];
+        auto rd = [&](int dt, int buf) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                vb[buf][ks][0] = lds_read_tr16_b64(va_addr[dt][0] + SOFF + ks * 16 * RB);
+                vb[buf][ks][1] = lds_read_tr16_b64(va_addr[dt][1] + SOFF + ks * 16 * RB);
+            }
+        };
+        rd(0, 0);
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            if (dt + 1 < NDT) {
+                rd(dt + 1, (dt + 1) & 1);
+                asm volatile("s_waitcnt lgkmcnt(4)" ::: "memory");
+            } else {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                tie(vb[dt & 1][ks][0]);
+                tie(vb[dt & 1][ks][1]);
+                const u32x2 a0 = vb[dt & 1][ks][0], a1 = vb[dt & 1][ks][1];
+                oacc[dt] = mfma32<F16>(u32x4{a0[0], a0[1], a1[0], a1[1]}, pk[ks], oacc[dt]);
+            }
+        }
+    };
+
+    // ---- main loop ----
+    // Request order: V(t) [tile t-2], K(t) [after QK(t-1)], V(t+1) [after
+    // PV(t-1)]: entering tile t, V(t+1) stays in flight.
+    issue_k(kreg, ta);
+    issue_v(0, ta);
+    issue_v(1, ta + 1);
+    constexpr int kLgkm0 = vm_wait(63) & ~(15 << 8);
+    for (int t = ta; t < tb; t += 2) {
+        __builtin_amdgcn_s_waitcnt(vm_wait(NI));
+        widen(0);
+        consume(Int<0>{}, t);
+        __builtin_amdgcn_s_waitcnt(kLgkm0);  // stage 0 read: refill it
+        issue_v(0, t + 2);
+        if (t + 1 >= tb) break;
+        __builtin_amdgcn_s_waitcnt(vm_wait(NI));
+        widen(1);
+        consume(Int<1>{}, t + 1);
+        __builtin_amdgcn_s_waitcnt(kLgkm0);
+        issue_v(1, t + 3);
+    }
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));
+
+    // ---- merge the 4 partials through LDS (each wave's own stages) ----
+    const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+    if (h2 == 0) { sm_ml[wave][c][0] = m_run; sm_ml[wave][c][1] = l_tot; }
+    // lane (c, h2) holds row c, d = dt*32 + g*8 + h2*4 + 0..3: chunk dt*8 + g*2 + h2,
+    // stored at chunk ^ (row % 16) of a D-float row.
+    const uint32_t pw = lds_addr(vst);
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            lds_write_b128(pw + c * D * 4 + (((dt * 8 + g * 2 + h2) ^ (c & 15)) * 16),
+                           __builtin_bit_cast(u32x4, f32x4{oacc[dt][g * 4], oacc[dt][g * 4 + 1],
+                                                           oacc[dt][g * 4 + 2], oacc[dt][g * 4 + 3]}));
+    __builtin_amdgcn_s_waitcnt(vm_wait(63) & ~(15 << 8));
+    __syncthreads();
+    // Wave w writes chunks [w*CPW, (w+1)*CPW) of every row, 64/CPW rows at a time.
+    constexpr int RPS = 64 / CPW;
+    const int ch = wave * CPW + lane % CPW;
+    for (int r0 = 0; r0 < 32; r0 += RPS) {
+        const int r = r0 + lane / CPW;
+        float mw[4], M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) { mw[w] = sm_ml[w][r][0]; M = fmaxf(M, mw[w]); }
+        const float mu = M == -INFINITY ? 0.f : M;
+        float L = 0.f;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        u32x4 pv[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+            pv[w] = lds_read_b128(lds_addr(lds + w * 2 * TILE) + r * D * 4 + ((ch ^ (r & 15)) * 16));
+        lds_wait_any();
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            tie(pv[w]);
+            const float a = __builtin_amdgcn_exp2f(mw[w] - mu);
+            L += sm_ml[w][r][1] * a;
+            acc += __builtin_bit_cast(f32x4, pv[w]) * a;
+        }
+        const float inv = L > 0.f ? 1.0f / L : 0.f;
+        if (q0 + r < S)
+            __builtin_nontemporal_store(acc * inv, (f32x4 *)(out + (int64_t)(q0 + r) * q_dim +
+                                                             (int64_t)head * D) + ch);
+    }
+}
+
+// head_dim 256: split-K inside one-wave-per-SIMD workgroups (the shared-ring
+// kernels need more than the 256 registers two waves per SIMD allow).
 template <class T, int D, bool V2 = (D <= 128)>
 struct PrefillLaunch {
     static void run(const void *q, const void *kc, const void *vc, int64_t kvs, int S, int sp,
                     int win, int nh, int kv_mul, float qs, float *out, hipStream_t st) {
-        const int nqb = (S + PrefillCfg<D>::BM - 1) / PrefillCfg<D>::BM;
-        const int total = nh * nqb;
+        const int nb = (S + 31) / 32;
+        const int total = nh * nb;
         const int per_xcd = (total + 7) / 8;
-        hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(per_xcd * 8), dim3(256), 0, st,
-                           (const uint16_t *)q, (const uint16_t *)kc, (const uint16_t *)vc, kvs,
-                           S, sp, win, nh, kv_mul, qs, out);
+        hipLaunchKernelGGL((prefill_sk_kernel<T, D>), dim3(per_xcd * 8), dim3(256), 0, st,
+                           (const uint16_t *)q, (const char *)kc, (const char *)vc, kvs, S, sp,
+                           win, nh, kv_mul, nb, qs, out);
     }
 };
 template <class T, int D>
