@@ -10,7 +10,7 @@ Also reported on the same line: causal prefill (configs[2], Qwen3-4B-shaped,
 S=2048 bf16) in TFLOP/s, long-context decode (configs[4], 32K bf16), the
 roofline of the dominant kernel and the CPU oracle on a bounded sample.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|long|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|long|append|copy]
 """
 from __future__ import annotations
 
@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "append", "copy"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     return ap.parse_args()
 
@@ -140,6 +140,52 @@ def bench_prefill(torch, A, args, S, H, Hk, D, dt):
     return dict(ms=ms, tflops=flop / (ms * 1e-3) / 1e12, flop=flop, launches=n)
 
 
+def bench_append(torch, A, args, S, H, Hk, D, dt):
+    """cfg3's fused append: S rows of f32 q/k/v -> Q/K RMSNorm -> NeoX RoPE
+    (theta 1e6) -> q (bf16) and the K/V cache rows (bf16).  HBM-bound: the
+    algorithmic bytes are the f32 rows read, the (cos, sin) rows read and the
+    bf16 rows written; timed as a graph of launches (no host overhead)."""
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(5)
+    q = torch.randn(S, H * D, generator=g, device=dev)
+    k = torch.randn(S, Hk * D, generator=g, device=dev)
+    v = torch.randn(S, Hk * D, generator=g, device=dev)
+    qn = 1.0 + 0.1 * torch.randn(D, generator=g, device=dev)
+    kn = 1.0 + 0.1 * torch.randn(D, generator=g, device=dev)
+    kc = torch.empty(S, Hk * D, dtype=dt, device=dev)
+    vc = torch.empty_like(kc)
+    qo = torch.empty(S, H * D, dtype=dt, device=dev)
+    cs = A.rope_table(S, D, 1e6)
+    run = lambda: A.qkv_append(q, k, v, kc, vc, cs, start_pos=0, n_head=H, n_kv_head=Hk,  # noqa: E731
+                               head_dim=D, q_norm=qn, k_norm=kn, q_out=qo)
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    reps = 20
+    gr = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(gr, stream=st):
+            for _ in range(reps):
+                run()
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    gr.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = max(3, min(args.steps // 20, 20))
+    t0.record()
+    for _ in range(n):
+        gr.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / (n * reps)
+    esz = torch.finfo(dt).bits // 8
+    nbytes = S * (H + 2 * Hk) * D * 4 + S * D * 4 + 2 * D * 4 + S * (H + 2 * Hk) * D * esz
+    return dict(us=us, bytes=nbytes, gbps=nbytes / (us * 1e3))
+
+
 def bench_copy(torch):
     """Plain copy of known size: the calibration kernel for FETCH/WRITE_SIZE."""
     n = 256 << 20
@@ -218,6 +264,8 @@ def main():
         res["cfg2"] = bench_decode(torch, A, args, 12, 2, 128, 4096, 28, torch.float16, "cfg2")
     if args.only in ("all", "prefill"):
         res["cfg3"] = bench_prefill(torch, A, args, 2048, 32, 8, 128, torch.bfloat16)
+    if args.only in ("all", "append"):
+        res["append"] = bench_append(torch, A, args, 2048, 32, 8, 128, torch.bfloat16)
     if args.only in ("all", "long"):
         res["cfg5"] = bench_decode(torch, A, argparse.Namespace(steps=max(5, args.steps // 10),
                                                                 warmup=3),
@@ -226,7 +274,7 @@ def main():
         print(json.dumps(res))
         return
 
-    d, p, lc = res["cfg2"], res["cfg3"], res["cfg5"]
+    d, p, lc, ap = res["cfg2"], res["cfg3"], res["cfg5"], res["append"]
     traffic = load_traffic()
     line = {
         "metric": METRIC,
@@ -259,6 +307,12 @@ def main():
                         "us_per_layer": round(lc["us_per_layer"], 3),
                         "gbps": round(lc["gbps_step"], 1),
                         "frac_hbm": round(lc["gbps_step"] / HBM_PEAK_GBS, 4)},
+        "append": {"workload": "cfg3 fused append: 2048 rows, 32/8 heads, head_dim 128, f32 "
+                               "q/k/v in, Q/K RMSNorm + NeoX RoPE, bf16 q and KV rows out",
+                   "kernel": "qkv_append_kernel<128,BF16,BF16>",
+                   "us": round(ap["us"], 3), "algorithmic_bytes": ap["bytes"],
+                   "gbps": round(ap["gbps"], 1),
+                   "frac_hbm": round(ap["gbps"] / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(d["gbps_step"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["gbps_step"] / HBM_PEAK_GBS, 4),

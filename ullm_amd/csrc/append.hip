@@ -1,30 +1,62 @@
 // Fused Q/K/V preparation + KV-cache append, and the host RoPE table.
 //
-// One wave owns one head vector of one token row:
+// A workgroup of kAppendWaves waves owns one token row; a row's head vectors
+// ("slots") are
 //   slots [0, n_head)                 -> a query head
 //   slots [n_head, n_head+n_kv_head)  -> a key head
 //   slots [.., n_head+2*n_kv_head)    -> a value head
-// and applies, in the reference's order (crates/ullm-model/src/lib.rs:
-// 1027-1058, decode :877-914): bias add, per-head RMSNorm (math.rs:82-86),
-// RoPE (math.rs:116-161) via the precomputed (cos, sin) table, then the
-// store -- q to q_out, K/V straight into the cache slot of position
-// start_pos + row.  This replaces the bias, rmsnorm_heads and rope_* Metal
-// dispatches (forward.rs:416-447, :799-853; shader.metal:828-941) with one
-// launch.
+// and wave w takes slots w, w + kAppendWaves, ..., kBatch at a time with
+// every load of a batch issued before any is used (the kernel streams
+// ~4 x D x 4 bytes per head and is HBM-bound).  Each slot gets, in the
+// reference's order (crates/ullm-model/src/lib.rs:1027-1058, decode
+// :877-914): bias add, per-head RMSNorm (math.rs:82-86), RoPE
+// (math.rs:116-161) via the precomputed (cos, sin) table, then the store --
+// q to q_out, K/V straight into the cache slot of position start_pos + row.
+// A lane holds D/64 consecutive elements (one 8-byte load for D = 128);
+// RoPE partners are exchanged through the wave's own LDS row.  This
+// replaces the bias, rmsnorm_heads and rope_* Metal dispatches
+// (forward.rs:416-447, :799-853; shader.metal:828-941) with one launch.
 #include <cmath>
 #include "common.hpp"
 #include "wave.hpp"
 
 namespace ullm {
 
-template <int OUT_DT>
-__device__ __forceinline__ void store_elem(void *base, int64_t idx, float v) {
-    if constexpr (OUT_DT == ULLM_DT_F32) ((float *)base)[idx] = v;
-    else if constexpr (OUT_DT == ULLM_DT_F16) ((uint16_t *)base)[idx] = f32_to_f16_bits(v);
-    else ((uint16_t *)base)[idx] = f32_to_bf16_bits(v);
+template <int N>
+struct VecF;
+template <> struct VecF<1> { typedef float t; };
+template <> struct VecF<2> { typedef float2 t; };
+template <> struct VecF<4> { typedef float4 t; };
+
+template <int E>
+__device__ __forceinline__ void load_e(const float *p, float (&x)[E]) {
+    if constexpr (E == 1) x[0] = p[0];
+    else if constexpr (E == 2) { const float2 v = *(const float2 *)p; x[0] = v.x; x[1] = v.y; }
+    else { const float4 v = *(const float4 *)p; x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w; }
+}
+
+// Store E consecutive elements converted to OUT_DT.
+template <int OUT_DT, int E>
+__device__ __forceinline__ void store_e(void *base, int64_t idx, const float (&x)[E]) {
+    if constexpr (OUT_DT == ULLM_DT_F32) {
+        float *p = (float *)base + idx;
+        if constexpr (E == 1) p[0] = x[0];
+        else if constexpr (E == 2) *(float2 *)p = float2{x[0], x[1]};
+        else *(float4 *)p = float4{x[0], x[1], x[2], x[3]};
+    } else {
+        // hardware round-to-nearest-even packs
+        auto pk = [](float a, float b) {
+            return OUT_DT == ULLM_DT_F16 ? pack_f16x2(a, b) : pack_bf16x2(a, b);
+        };
+        uint16_t *p = (uint16_t *)base + idx;
+        if constexpr (E == 1) p[0] = (uint16_t)pk(x[0], 0.f);
+        else if constexpr (E == 2) *(uint32_t *)p = pk(x[0], x[1]);
+        else *(uint2 *)p = uint2{pk(x[0], x[1]), pk(x[2], x[3])};
+    }
 }
 
 constexpr int kAppendWaves = 4;
+constexpr int kBatch = 4;  // slots per wave with loads in flight together
 
 template <int D, int QDT, int KVDT>
 __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
@@ -34,71 +66,123 @@ __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
     const float *__restrict__ k_norm, float eps, const float *__restrict__ cs, int neox,
     int rotary_dim, int rows, int start_pos, int n_head, int n_kv_head, void *q_out,
     void *k_cache, void *v_cache, int64_t kv_stride) {
-    constexpr int NE = D / 64;
+    constexpr int E = D / 64;
     __shared__ float buf[kAppendWaves][D];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: slot math in SGPRs
+    const int row = blockIdx.x;
     const int slots = n_head + 2 * n_kv_head;
-    const int64_t gslot = (int64_t)blockIdx.x * kAppendWaves + wave;
-    const bool active = gslot < (int64_t)rows * slots;
-    const int row = active ? (int)(gslot / slots) : 0;
-    const int slot = active ? (int)(gslot % slots) : 0;
-    const int kind = slot < n_head ? 0 : (slot < n_head + n_kv_head ? 1 : 2);
-    const int head = kind == 0 ? slot : (kind == 1 ? slot - n_head : slot - n_head - n_kv_head);
     const int64_t q_dim = (int64_t)n_head * D, kv_dim = (int64_t)n_kv_head * D;
-    const float *src = kind == 0 ? q_in + row * q_dim : (kind == 1 ? k_in : v_in) + row * kv_dim;
-    src += (int64_t)head * D;
-    const float *bias = kind == 0 ? q_bias : (kind == 1 ? k_bias : v_bias);
-    const float *nw = kind == 0 ? q_norm : (kind == 1 ? k_norm : nullptr);
-
-    float x[NE];
-#pragma unroll
-    for (int i = 0; i < NE; i++) {
-        const int e = lane + 64 * i;
-        x[i] = active ? src[e] : 0.f;
-        if (bias) x[i] += bias[(int64_t)head * D + e];
-    }
-    if (nw) {
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < NE; i++) ss += x[i] * x[i];
-        ss = group_sum<64>(ss);
-        const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-#pragma unroll
-        for (int i = 0; i < NE; i++) x[i] = x[i] * inv * nw[lane + 64 * i];
-    }
     const int pos = start_pos + row;
-    // RoPE needs the partner element of each pair: exchange through LDS.
-#pragma unroll
-    for (int i = 0; i < NE; i++) buf[wave][lane + 64 * i] = x[i];
-    __syncthreads();
-    if (kind != 2) {
-        const int half = rotary_dim / 2;
+    const int e0 = lane * E;  // this lane's first element
+
+    // (cos, sin) of this lane's elements, shared by every rotated head of the row.
+    const int half = rotary_dim / 2;
+    float rc[E], rs[E];
+    {
         const float *cp = cs + (int64_t)pos * half * 2;
 #pragma unroll
-        for (int i = 0; i < NE; i++) {
-            const int e = lane + 64 * i;
-            if (neox) {
-                if (e < rotary_dim) {
-                    const int j = e < half ? e : e - half;
-                    const float c = cp[2 * j], s = cp[2 * j + 1];
-                    const float a = buf[wave][j], b = buf[wave][j + half];
-                    x[i] = e < half ? a * c - b * s : a * s + b * c;
-                }
-            } else if (e < rotary_dim) {
-                const int j = e >> 1;
-                const float c = cp[2 * j], s = cp[2 * j + 1];
-                const float a = buf[wave][e & ~1], b = buf[wave][e | 1];
-                x[i] = (e & 1) ? a * s + b * c : a * c - b * s;
-            }
+        for (int i = 0; i < E; i++) {
+            const int e = e0 + i;
+            const int j = e < rotary_dim ? (neox ? (e < half ? e : e - half) : e >> 1) : 0;
+            rc[i] = cp[2 * j];
+            rs[i] = cp[2 * j + 1];
         }
     }
-    if (!active) return;
+
+    const bool full_rot = rotary_dim == D;
+    float rope_y[E];
+    // Norm weights of this lane's elements (q and k), loaded once.
+    float wq[E], wk[E];
 #pragma unroll
-    for (int i = 0; i < NE; i++) {
-        const int e = lane + 64 * i;
-        if (kind == 0) store_elem<QDT>(q_out, row * q_dim + (int64_t)head * D + e, x[i]);
-        else store_elem<KVDT>(kind == 1 ? k_cache : v_cache,
-                              (int64_t)pos * kv_stride + (int64_t)head * D + e, x[i]);
+    for (int i = 0; i < E; i++) { wq[i] = 1.f; wk[i] = 1.f; }
+    if (q_norm) load_e<E>(q_norm + e0, wq);
+    if (k_norm) load_e<E>(k_norm + e0, wk);
+
+    for (int s0 = wave; s0 < slots; s0 += kAppendWaves * kBatch) {
+        float x[kBatch][E], bv[kBatch][E];
+        int kind[kBatch], head[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; b++) {
+            const int slot = s0 + b * kAppendWaves;
+            const bool ok = slot < slots;
+            kind[b] = !ok ? 3 : (slot < n_head ? 0 : (slot < n_head + n_kv_head ? 1 : 2));
+            head[b] = kind[b] == 0 ? slot : (kind[b] == 1 ? slot - n_head : slot - n_head - n_kv_head);
+            const float *src = kind[b] == 0 ? q_in + row * q_dim : (kind[b] == 1 ? k_in : v_in) + row * kv_dim;
+            const float *bias = kind[b] == 0 ? q_bias : (kind[b] == 1 ? k_bias : v_bias);
+            if (ok) load_e<E>(src + (int64_t)head[b] * D + e0, x[b]);
+            else
+#pragma unroll
+                for (int i = 0; i < E; i++) x[b][i] = 0.f;
+            if (ok && bias) load_e<E>(bias + (int64_t)head[b] * D + e0, bv[b]);
+            else
+#pragma unroll
+                for (int i = 0; i < E; i++) bv[b][i] = 0.f;
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; b++) {
+            if (kind[b] == 3) continue;  // wave-uniform
+#pragma unroll
+            for (int i = 0; i < E; i++) x[b][i] += bv[b][i];
+            const float *nw = kind[b] == 0 ? q_norm : (kind[b] == 1 ? k_norm : nullptr);
+            if (nw) {
+                float ss = 0.f;
+#pragma unroll
+                for (int i = 0; i < E; i++) ss += x[b][i] * x[b][i];
+                ss = wave_sum(ss);
+                // v_rsq_f32 (~1 ulp) for (sum/n + eps).sqrt().recip()
+                const float inv = __builtin_amdgcn_rsqf(ss / (float)D + eps);
+#pragma unroll
+                for (int i = 0; i < E; i++) x[b][i] = x[b][i] * inv * (kind[b] == 0 ? wq[i] : wk[i]);
+            }
+            if (kind[b] != 2 && full_rot) {
+                // Full-width RoPE: a NeoX partner (e +- D/2) sits in lane l ^ 32
+                // at the same element index; an interleaved partner (e ^ 1) in
+                // the same lane, or in lane l ^ 1 when a lane holds one element.
+#pragma unroll
+                for (int i = 0; i < E; i++) {
+                    float pa;
+                    if (neox) pa = xor32(x[b][i]);
+                    else if constexpr (E == 1) pa = dpp<kDppXor1>(x[b][i]);
+                    else pa = x[b][i ^ 1];
+                    const bool lo = neox ? lane < 32 : ((e0 + i) & 1) == 0;
+                    // lo: a*c - b*s with a = own, b = partner; hi: a*s + b*c with a = partner
+                    rope_y[i] = lo ? x[b][i] * rc[i] - pa * rs[i] : pa * rs[i] + x[b][i] * rc[i];
+                }
+#pragma unroll
+                for (int i = 0; i < E; i++) x[b][i] = rope_y[i];
+            } else if (kind[b] != 2) {
+                // Partial rotary: the partner of each pair comes from the
+                // wave's LDS row (LDS operations of one wave complete in order).
+#pragma unroll
+                for (int i = 0; i < E; i++) buf[wave][e0 + i] = x[b][i];
+                __builtin_amdgcn_wave_barrier();
+                float y[E];
+#pragma unroll
+                for (int i = 0; i < E; i++) {
+                    const int e = e0 + i;
+                    y[i] = x[b][i];
+                    if (e < rotary_dim) {
+                        if (neox) {
+                            const int j = e < half ? e : e - half;
+                            const float a = buf[wave][j], c = buf[wave][j + half];
+                            y[i] = e < half ? a * rc[i] - c * rs[i] : a * rs[i] + c * rc[i];
+                        } else {
+                            const float a = buf[wave][e & ~1], c = buf[wave][e | 1];
+                            y[i] = (e & 1) ? a * rs[i] + c * rc[i] : a * rc[i] - c * rs[i];
+                        }
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();  // the row is rewritten by the next slot
+#pragma unroll
+                for (int i = 0; i < E; i++) x[b][i] = y[i];
+            }
+            if (kind[b] == 0)
+                store_e<QDT, E>(q_out, row * q_dim + (int64_t)head[b] * D + e0, x[b]);
+            else
+                store_e<KVDT, E>(kind[b] == 1 ? k_cache : v_cache,
+                                 (int64_t)pos * kv_stride + (int64_t)head[b] * D + e0, x[b]);
+        }
     }
 }
 
@@ -180,8 +264,7 @@ extern "C" int ullm_hip_qkv_append(const float *q_in, const float *k_in, const f
                          rope_n_pos, start_pos + rows);
     if (q_out == (void *)q_in && q_dtype != ULLM_DT_F32)
         return set_error(ULLM_HIP_E_INVALID, "qkv_append: in-place q needs q_dtype f32");
-    const int64_t waves = (int64_t)rows * (n_head + 2 * n_kv_head);
-    dim3 grid((unsigned)((waves + kAppendWaves - 1) / kAppendWaves)), block(kAppendWaves * 64);
+    dim3 grid((unsigned)rows), block(kAppendWaves * 64);
     hipStream_t st = (hipStream_t)stream;
     switch (head_dim) {
         case 64: launch_q<64>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride); break;

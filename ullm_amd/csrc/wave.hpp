@@ -26,4 +26,23 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
+// Full-wave sum in VALU only: DPP inside 16-lane rows, then the gfx950 lane
+// swaps across rows (x + the lane 16 / 32 away); every lane gets the total.
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp<kDppXor1>(x);
+    x += dpp<kDppXor2>(x);
+    x += dpp<kDppHalfMirror>(x);
+    x += dpp<kDppMirror>(x);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// The value of lane l ^ 32.
+__device__ __forceinline__ float xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+}
+
 }  // namespace ullm
