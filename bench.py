@@ -10,7 +10,7 @@ Also reported on the same line: causal prefill (configs[2], Qwen3-4B-shaped,
 S=2048 bf16) in TFLOP/s, long-context decode (configs[4], 32K bf16), the
 roofline of the dominant kernel and the CPU oracle on a bounded sample.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|long|append|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|long|append|proj|copy]
 """
 from __future__ import annotations
 
@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "append", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "append", "proj", "copy"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     return ap.parse_args()
 
@@ -186,6 +186,55 @@ def bench_append(torch, A, args, S, H, Hk, D, dt):
     return dict(us=us, bytes=nbytes, gbps=nbytes / (us * 1e3))
 
 
+def bench_proj(torch, A, args, hidden, H, Hk, D, wdt):
+    """Decode-side Q/K/V projection + fused append for one token (Qwen3-4B
+    shape): HBM-bound on the weights.  Algorithmic bytes = the three weight
+    matrices + x + the outputs; timed as a graph of launches, the weights
+    rotated over enough copies to exceed the MALL."""
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(11)
+    wbytes = (H + 2 * Hk) * D * hidden * torch.finfo(wdt).bits // 8
+    n_sets = max(1, math.ceil(2 * MALL_BYTES / wbytes))
+    sets = []
+    for _ in range(n_sets):
+        sets.append(tuple((0.02 * torch.randn(n * D, hidden, generator=g, device=dev)).to(wdt)
+                          for n in (H, Hk, Hk)))
+    x = torch.randn(1, hidden, generator=g, device=dev)
+    qn = 1.0 + 0.1 * torch.randn(D, generator=g, device=dev)
+    kn = 1.0 + 0.1 * torch.randn(D, generator=g, device=dev)
+    n_ctx = 4096
+    kc = torch.zeros(n_ctx, Hk * D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    qo = torch.empty(1, H * D, device=dev)
+    cs = A.rope_table(n_ctx, D, 1e6)
+    run = lambda si: A.qkv_proj_append(x, *sets[si], kc, vc, cs, start_pos=n_ctx - 1, n_head=H,  # noqa: E731
+                                       n_kv_head=Hk, head_dim=D, q_norm=qn, k_norm=kn, q_out=qo)
+    for si in range(n_sets):
+        run(si)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(gr, stream=st):
+            for si in range(n_sets):
+                run(si)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    gr.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = max(3, min(args.steps // 20, 20))
+    t0.record()
+    for _ in range(n):
+        gr.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / (n * n_sets)
+    nbytes = wbytes + hidden * 4 + H * D * 4 + 2 * Hk * D * 2
+    return dict(us=us, bytes=nbytes, gbps=nbytes / (us * 1e3), n_sets=n_sets)
+
+
 def bench_copy(torch):
     """Plain copy of known size: the calibration kernel for FETCH/WRITE_SIZE."""
     n = 256 << 20
@@ -266,6 +315,8 @@ def main():
         res["cfg3"] = bench_prefill(torch, A, args, 2048, 32, 8, 128, torch.bfloat16)
     if args.only in ("all", "append"):
         res["append"] = bench_append(torch, A, args, 2048, 32, 8, 128, torch.bfloat16)
+    if args.only in ("all", "proj"):
+        res["proj"] = bench_proj(torch, A, args, 2560, 32, 8, 128, torch.bfloat16)
     if args.only in ("all", "long"):
         res["cfg5"] = bench_decode(torch, A, argparse.Namespace(steps=max(5, args.steps // 10),
                                                                 warmup=3),
@@ -274,7 +325,7 @@ def main():
         print(json.dumps(res))
         return
 
-    d, p, lc, ap = res["cfg2"], res["cfg3"], res["cfg5"], res["append"]
+    d, p, lc, ap, pj = res["cfg2"], res["cfg3"], res["cfg5"], res["append"], res["proj"]
     traffic = load_traffic()
     line = {
         "metric": METRIC,
@@ -313,6 +364,13 @@ def main():
                    "us": round(ap["us"], 3), "algorithmic_bytes": ap["bytes"],
                    "gbps": round(ap["gbps"], 1),
                    "frac_hbm": round(ap["gbps"] / HBM_PEAK_GBS, 4)},
+        "qkv_proj": {"workload": "Qwen3-4B-shaped decode Q/K/V projection + fused append: "
+                                 "hidden 2560, 32/8 heads, head_dim 128, bf16 weights, Q/K "
+                                 "RMSNorm + NeoX RoPE, bf16 cache",
+                     "kernel": "qkv_proj_kernel<128,BF16,F32,BF16>",
+                     "us": round(pj["us"], 3), "algorithmic_bytes": pj["bytes"],
+                     "gbps": round(pj["gbps"], 1),
+                     "frac_hbm": round(pj["gbps"] / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(d["gbps_step"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["gbps_step"] / HBM_PEAK_GBS, 4),

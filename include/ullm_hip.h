@@ -130,6 +130,27 @@ int ullm_hip_qkv_append(const float *q_in, const float *k_in, const float *v_in,
                         void *q_out, int q_dtype, void *k_cache, void *v_cache, int kv_dtype,
                         int64_t kv_stride, void *stream);
 
+/* Decode-side Q/K/V projection with the append fused into its epilogue, for
+ * `rows` tokens at positions start_pos..: computes lib.rs:857-914 (the
+ * non-gated attention path) and replaces the Metal forward's wq/wk/wv matvecs
+ * into q and the cache slot plus the bias / rmsnorm_heads / rope dispatches
+ * (forward.rs:415-447):
+ *   q = W_q x, k = W_k x, v = W_v x      (math.rs:9-21 matvec_q, f32 sums)
+ * followed by exactly what ullm_hip_qkv_append does to q, k and v.
+ * x:   [rows][in_dim] f32 (the attention-normed hidden state), DEVICE
+ * w_q: [n_head*head_dim][in_dim], w_k / w_v: [n_kv_head*head_dim][in_dim],
+ *      row-major, w_dtype f32, f16 or bf16 (other weight formats: unsupported)
+ * in_dim a multiple of 8; x and the weights 16-byte aligned; rows <= 65535.
+ * One workgroup per (head vector, row): HBM-bound on the weights. */
+int ullm_hip_qkv_proj_append(const float *x, int in_dim, const void *w_q, const void *w_k,
+                             const void *w_v, int w_dtype, const float *q_bias,
+                             const float *k_bias, const float *v_bias, const float *q_norm,
+                             const float *k_norm, float eps, const float *rope_cs,
+                             int rope_n_pos, int rope_neox, int rotary_dim, int rows,
+                             int start_pos, int n_head, int n_kv_head, int head_dim, void *q_out,
+                             int q_dtype, void *k_cache, void *v_cache, int kv_dtype,
+                             int64_t kv_stride, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,7 @@ def lib() -> C.CDLL:
         h.ora_qkv_append.argtypes = [_f, _f, _f, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                      C.c_int, _f, _f, _f, _f, _f, C.c_float, C.c_int, C.c_float,
                                      _f, _f, C.c_size_t]
+        h.ora_matvec.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, _f, _f]
         _lib = h
     return _lib
 
@@ -134,3 +135,15 @@ def qkv_append(q, k, v, start_pos, n_head, n_kv_head, head_dim, rotary_dim, thet
                              _p(q_norm), _p(k_norm), eps, int(bool(neox)), theta, _p(kc), _p(vc),
                              kv_stride))
     return qo
+
+
+def matvec(w_raw: np.ndarray, dtype: int, x: np.ndarray) -> np.ndarray:
+    """math.rs:9-21 (matvec_q): y = W x with W [out][cols] in f32 (dtype 0)
+    or raw uint16 f16 (1) / bf16 (2) storage; sequential f32 sums."""
+    w_raw = np.ascontiguousarray(w_raw)
+    out, cols = w_raw.shape
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.size == cols
+    y = np.empty(out, dtype=np.float32)
+    _rc(lib().ora_matvec(w_raw.ctypes.data_as(C.c_void_p), dtype, out, cols, _p(x), _p(y)))
+    return y

@@ -258,3 +258,25 @@ int ora_qkv_append(float *q, const float *k, const float *v, int rows, int start
     free(kb); free(vb); free(tmp);
     return 0;
 }
+
+/* crates/ullm-model/src/math.rs:9-21 -- matvec_q for an f32/f16/bf16 weight:
+ * for every output row o, dequantize row o (dequant.rs:61-94) and
+ *   y[o] = sum_i w[o][i] * x[i]      (a left fold from 0.0, one rounding per
+ *                                      product and per add: Rust's `.sum()`)
+ * w: [out][cols] raw storage (f32 or 16-bit), x: [cols], y: [out]. */
+int ora_matvec(const void *w, int dtype, int out, int cols, const float *x, float *y) {
+    float *row = (float *)malloc(sizeof(float) * (size_t)cols);
+    if (!row) return -2;
+    const size_t esz = dtype == ORA_F32 ? 4 : 2;
+    for (int o = 0; o < out; o++) {
+        ora_widen((const char *)w + (size_t)o * cols * esz, dtype, (size_t)cols, row);
+        float acc = 0.0f;
+        for (int i = 0; i < cols; i++) {
+            const float p = row[i] * x[i];
+            acc = acc + p;
+        }
+        y[o] = acc;
+    }
+    free(row);
+    return 0;
+}

@@ -95,3 +95,24 @@ def test_workspace_size_planning():
     assert ws(1, 12, 2, 128, 64, 0) == 0  # one split: no partials
     assert ws(1, 32, 4, 128, 32768, 0) >= ws(1, 32, 4, 128, 4096, 0)
     assert ws(1, 12, 5, 128, 4096, 0) == 0  # invalid shape
+
+
+def test_proj_append_validation():
+    f = L.lib().ullm_hip_qkv_proj_append
+
+    def call(**kw):
+        a = dict(x=None, in_dim=1536, wq=None, wk=None, wv=None, wdt=L.DT_BF16, qb=None, kb=None,
+                 vb=None, qn=None, kn=None, eps=1e-6, cs=None, npos=10, neox=1, rd=128, rows=1,
+                 sp=0, h=12, hk=2, d=128, qo=None, qdt=L.DT_F32, kc=None, vc=None,
+                 kvdt=L.DT_F16, kvs=256, st=None)
+        a.update(kw)
+        return f(*a.values())
+
+    assert call(wdt=7) == L.E_UNSUPPORTED
+    assert call(d=96) == L.E_UNSUPPORTED
+    assert call(hk=5) == L.E_INVALID
+    assert call(in_dim=1540) == L.E_INVALID  # not a multiple of 8
+    assert call(rd=3) == L.E_INVALID
+    assert call(kvs=100) == L.E_INVALID
+    assert call(rows=0) == L.OK  # nothing to do
+    assert call() == L.E_INVALID  # null pointers

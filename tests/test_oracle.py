@@ -245,3 +245,45 @@ def test_split_kv_merge_math():
     num = sum(acc * np.exp(m - M) for m, _, acc in parts)
     den = sum(l * np.exp(m - M) for m, l, _ in parts)
     np.testing.assert_allclose(num / den, f64_attention(q, k, v, 1.0), rtol=1e-12)
+
+
+# --- matvec (math.rs:9-21) --------------------------------------------------------
+
+def test_matvec_reference_cases():
+    # math.rs:192-205 matvec_q_f32_identity
+    eye = np.array([[1.0, 0.0], [0.0, 1.0]], dtype=np.float32)
+    np.testing.assert_array_equal(ora.matvec(eye, 0, np.array([3.0, 5.0], np.float32)), [3.0, 5.0])
+    # math.rs:208-233: the stacked per-token matvecs of a 3x2 weight
+    w = np.array([[1.0, 2.0], [3.0, 4.0], [-1.0, 0.5]], dtype=np.float32)
+    xs = np.array([[1.0, 0.0], [0.5, -2.0], [3.0, 3.0]], dtype=np.float32)
+    want = [[1.0, 3.0, -1.0], [-3.5, -6.5, -1.5], [9.0, 21.0, -1.5]]
+    for x, y in zip(xs, want):
+        np.testing.assert_array_equal(ora.matvec(w, 0, x), y)
+
+
+def test_matvec_left_fold_order():
+    # A sequential f32 sum drops the 1 next to 1e8 before the cancellation;
+    # any reordering (pairwise, tree, f64) returns 1.
+    w = np.array([[1e8, 1.0, -1e8]], dtype=np.float32)
+    assert ora.matvec(w, 0, np.ones(3, np.float32))[0] == 0.0
+
+
+@pytest.mark.parametrize("dtype", [0, 1, 2])
+def test_matvec_matches_f64(dtype):
+    out, cols = 37, 300
+    wf = (0.05 * RNG.standard_normal((out, cols))).astype(np.float32)
+    if dtype == 0:
+        raw, wexact = wf, wf.astype(np.float64)
+    elif dtype == 1:
+        raw = wf.astype(np.float16).view(np.uint16)
+        wexact = raw.view(np.float16).astype(np.float64)
+    else:
+        raw = (torch.from_numpy(wf).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16))
+        wexact = torch.from_numpy(raw.view(np.int16)).view(torch.bfloat16).double().numpy()
+    x = RNG.standard_normal(cols).astype(np.float32)
+    y = ora.matvec(raw, dtype, x)
+    ref = wexact @ x.astype(np.float64)
+    bound = cols * np.finfo(np.float32).eps * (np.abs(wexact) @ np.abs(x.astype(np.float64)))
+    assert np.all(np.abs(y - ref) <= bound)
+    # transposed operand or a row offset would fail this
+    assert np.abs(y - ref).max() < 1e-4

@@ -32,6 +32,11 @@ SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _i, _i, _i, _i, _i,
          _vp, _i, _vp, _vp, _i, _i64, _vp],
     ),
+    "ullm_hip_qkv_proj_append": (
+        _i,
+        [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _i, _i, _i,
+         _i, _i, _vp, _i, _vp, _vp, _i, _i64, _vp],
+    ),
 }
 
 

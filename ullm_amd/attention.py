@@ -147,6 +147,39 @@ def qkv_append(q, k, v, k_cache, v_cache, rope_cs, *, start_pos, n_head, n_kv_he
     return q_out
 
 
+def qkv_proj_append(x, w_q, w_k, w_v, k_cache, v_cache, rope_cs, *, start_pos, n_head,
+                    n_kv_head, head_dim, rotary_dim=None, neox=True, q_norm=None, k_norm=None,
+                    eps=1e-6, q_bias=None, k_bias=None, v_bias=None, q_out=None, q_dtype=None,
+                    kv_stride=None, stream=None):
+    """Q/K/V projection (matvec_q, math.rs:9-21) with the append fused in
+    (lib.rs:857-914).  x: [rows, in_dim] f32; w_*: [out, in_dim] f32/f16/bf16.
+    Returns q_out ([rows, n_head*D], q_dtype); K/V land in the cache."""
+    rows, in_dim = x.shape
+    _need_cuda(x, w_q, w_k, w_v, k_cache, v_cache, rope_cs)
+    if x.dtype != torch.float32 or not x.is_contiguous():
+        raise L.UllmHipError(L.E_INVALID, "x must be contiguous f32")
+    if not (w_q.dtype == w_k.dtype == w_v.dtype):
+        raise L.UllmHipError(L.E_INVALID, "w_q/w_k/w_v must share one dtype")
+    for w, n in ((w_q, n_head), (w_k, n_kv_head), (w_v, n_kv_head)):
+        if tuple(w.shape) != (n * head_dim, in_dim) or not w.is_contiguous():
+            raise L.UllmHipError(L.E_INVALID, f"weight shape {tuple(w.shape)} != ({n * head_dim}, {in_dim})")
+    if rotary_dim is None:
+        rotary_dim = head_dim
+    if q_dtype is None:
+        q_dtype = torch.float32
+    if q_out is None:
+        q_out = torch.empty(rows, n_head * head_dim, dtype=q_dtype, device=x.device)
+    if kv_stride is None:
+        kv_stride = n_kv_head * head_dim
+    rc = L.lib().ullm_hip_qkv_proj_append(
+        _ptr(x), in_dim, _ptr(w_q), _ptr(w_k), _ptr(w_v), _dt(w_q), _ptr(q_bias), _ptr(k_bias),
+        _ptr(v_bias), _ptr(q_norm), _ptr(k_norm), float(eps), _ptr(rope_cs), rope_cs.shape[0],
+        int(bool(neox)), rotary_dim, rows, start_pos, n_head, n_kv_head, head_dim, _ptr(q_out),
+        _DT[q_out.dtype], _ptr(k_cache), _ptr(v_cache), _dt(k_cache), kv_stride, _stream(stream))
+    L.check(rc)
+    return q_out
+
+
 @dataclass
 class AttnParams:
     """The attention fields of the reference's GpuParams (forward.rs:23-51)."""

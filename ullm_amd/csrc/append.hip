@@ -58,6 +58,109 @@ __device__ __forceinline__ void store_e(void *base, int64_t idx, const float (&x
 constexpr int kAppendWaves = 4;
 constexpr int kBatch = 4;  // slots per wave with loads in flight together
 
+// Per-lane state of the head epilogue of one token row: the (cos, sin) of
+// this lane's elements at the row's position and the Q/K norm weights.  A
+// lane holds E = D/64 consecutive elements of a head vector.
+template <int D>
+struct HeadEpi {
+    static constexpr int E = D / 64;
+    int lane, e0, rotary_dim, half, neox;
+    float eps;
+    float rc[E], rs[E], wq[E], wk[E];
+    const float *q_norm, *k_norm;
+
+    __device__ __forceinline__ HeadEpi(const float *cs, int pos, int rotary_dim_, int neox_,
+                                       const float *qn, const float *kn, float eps_)
+        : lane((int)(threadIdx.x & 63)), e0((int)(threadIdx.x & 63) * E), rotary_dim(rotary_dim_),
+          half(rotary_dim_ / 2), neox(neox_), eps(eps_), q_norm(qn), k_norm(kn) {
+        const float *cp = cs + (int64_t)pos * half * 2;
+#pragma unroll
+        for (int i = 0; i < E; i++) {
+            const int e = e0 + i;
+            const int j = e < rotary_dim ? (neox ? (e < half ? e : e - half) : e >> 1) : 0;
+            rc[i] = cp[2 * j];
+            rs[i] = cp[2 * j + 1];
+            wq[i] = 1.f;
+            wk[i] = 1.f;
+        }
+        if (q_norm) load_e<E>(q_norm + e0, wq);
+        if (k_norm) load_e<E>(k_norm + e0, wk);
+    }
+
+    // Bias (already added by the caller), per-head RMSNorm (math.rs:82-86)
+    // and RoPE (math.rs:116-161) of one head vector of kind 0 (q), 1 (k) or
+    // 2 (v), in the reference's order.  lds_row: D floats private to the
+    // wave, used only for partial-rotary pairs.
+    __device__ __forceinline__ void norm_rope(float (&x)[E], int kind, float *lds_row) const {
+        const float *nw = kind == 0 ? q_norm : (kind == 1 ? k_norm : nullptr);
+        if (nw) {
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < E; i++) ss += x[i] * x[i];
+            ss = wave_sum(ss);
+            // v_rsq_f32 (~1 ulp) for (sum/n + eps).sqrt().recip()
+            const float inv = __builtin_amdgcn_rsqf(ss / (float)D + eps);
+#pragma unroll
+            for (int i = 0; i < E; i++) x[i] = x[i] * inv * (kind == 0 ? wq[i] : wk[i]);
+        }
+        if (kind == 2) return;
+        float y[E];
+        if (rotary_dim == D) {
+            // Full-width RoPE: a NeoX partner (e +- D/2) sits in lane l ^ 32 at
+            // the same element index; an interleaved partner (e ^ 1) in the same
+            // lane, or in lane l ^ 1 when a lane holds one element.
+#pragma unroll
+            for (int i = 0; i < E; i++) {
+                float pa;
+                if (neox) pa = xor32(x[i]);
+                else if constexpr (E == 1) pa = dpp<kDppXor1>(x[i]);
+                else pa = x[i ^ 1];
+                const bool lo = neox ? lane < 32 : ((e0 + i) & 1) == 0;
+                // lo: a*c - b*s with a = own, b = partner; hi: a*s + b*c with a = partner
+                y[i] = lo ? x[i] * rc[i] - pa * rs[i] : pa * rs[i] + x[i] * rc[i];
+            }
+        } else {
+            // Partial rotary: the partner of each pair comes from the wave's
+            // LDS row (LDS operations of one wave complete in order).
+#pragma unroll
+            for (int i = 0; i < E; i++) lds_row[e0 + i] = x[i];
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int i = 0; i < E; i++) {
+                const int e = e0 + i;
+                y[i] = x[i];
+                if (e < rotary_dim) {
+                    if (neox) {
+                        const int j = e < half ? e : e - half;
+                        const float a = lds_row[j], c = lds_row[j + half];
+                        y[i] = e < half ? a * rc[i] - c * rs[i] : a * rs[i] + c * rc[i];
+                    } else {
+                        const float a = lds_row[e & ~1], c = lds_row[e | 1];
+                        y[i] = (e & 1) ? a * rs[i] + c * rc[i] : a * rc[i] - c * rs[i];
+                    }
+                }
+            }
+            __builtin_amdgcn_wave_barrier();  // the row may be rewritten next
+        }
+#pragma unroll
+        for (int i = 0; i < E; i++) x[i] = y[i];
+    }
+};
+
+// Store one finished head vector: q to q_out (row-major [rows][n_head*D]),
+// k / v into the cache row of position pos.
+template <int D, int QDT, int KVDT>
+__device__ __forceinline__ void store_head(const float (&x)[D / 64], int kind, int head, int row,
+                                           int pos, int e0, int64_t q_dim, void *q_out,
+                                           void *k_cache, void *v_cache, int64_t kv_stride) {
+    constexpr int E = D / 64;
+    if (kind == 0)
+        store_e<QDT, E>(q_out, row * q_dim + (int64_t)head * D + e0, x);
+    else
+        store_e<KVDT, E>(kind == 1 ? k_cache : v_cache,
+                         (int64_t)pos * kv_stride + (int64_t)head * D + e0, x);
+}
+
 template <int D, int QDT, int KVDT>
 __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
     const float *__restrict__ q_in, const float *__restrict__ k_in, const float *__restrict__ v_in,
@@ -68,36 +171,13 @@ __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
     void *k_cache, void *v_cache, int64_t kv_stride) {
     constexpr int E = D / 64;
     __shared__ float buf[kAppendWaves][D];
-    const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: slot math in SGPRs
     const int row = blockIdx.x;
     const int slots = n_head + 2 * n_kv_head;
     const int64_t q_dim = (int64_t)n_head * D, kv_dim = (int64_t)n_kv_head * D;
     const int pos = start_pos + row;
-    const int e0 = lane * E;  // this lane's first element
-
-    // (cos, sin) of this lane's elements, shared by every rotated head of the row.
-    const int half = rotary_dim / 2;
-    float rc[E], rs[E];
-    {
-        const float *cp = cs + (int64_t)pos * half * 2;
-#pragma unroll
-        for (int i = 0; i < E; i++) {
-            const int e = e0 + i;
-            const int j = e < rotary_dim ? (neox ? (e < half ? e : e - half) : e >> 1) : 0;
-            rc[i] = cp[2 * j];
-            rs[i] = cp[2 * j + 1];
-        }
-    }
-
-    const bool full_rot = rotary_dim == D;
-    float rope_y[E];
-    // Norm weights of this lane's elements (q and k), loaded once.
-    float wq[E], wk[E];
-#pragma unroll
-    for (int i = 0; i < E; i++) { wq[i] = 1.f; wk[i] = 1.f; }
-    if (q_norm) load_e<E>(q_norm + e0, wq);
-    if (k_norm) load_e<E>(k_norm + e0, wk);
+    const HeadEpi<D> epi(cs, pos, rotary_dim, neox, q_norm, k_norm, eps);
+    const int e0 = epi.e0;
 
     for (int s0 = wave; s0 < slots; s0 += kAppendWaves * kBatch) {
         float x[kBatch][E], bv[kBatch][E];
@@ -124,66 +204,129 @@ __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
             if (kind[b] == 3) continue;  // wave-uniform
 #pragma unroll
             for (int i = 0; i < E; i++) x[b][i] += bv[b][i];
-            const float *nw = kind[b] == 0 ? q_norm : (kind[b] == 1 ? k_norm : nullptr);
-            if (nw) {
-                float ss = 0.f;
-#pragma unroll
-                for (int i = 0; i < E; i++) ss += x[b][i] * x[b][i];
-                ss = wave_sum(ss);
-                // v_rsq_f32 (~1 ulp) for (sum/n + eps).sqrt().recip()
-                const float inv = __builtin_amdgcn_rsqf(ss / (float)D + eps);
-#pragma unroll
-                for (int i = 0; i < E; i++) x[b][i] = x[b][i] * inv * (kind[b] == 0 ? wq[i] : wk[i]);
-            }
-            if (kind[b] != 2 && full_rot) {
-                // Full-width RoPE: a NeoX partner (e +- D/2) sits in lane l ^ 32
-                // at the same element index; an interleaved partner (e ^ 1) in
-                // the same lane, or in lane l ^ 1 when a lane holds one element.
-#pragma unroll
-                for (int i = 0; i < E; i++) {
-                    float pa;
-                    if (neox) pa = xor32(x[b][i]);
-                    else if constexpr (E == 1) pa = dpp<kDppXor1>(x[b][i]);
-                    else pa = x[b][i ^ 1];
-                    const bool lo = neox ? lane < 32 : ((e0 + i) & 1) == 0;
-                    // lo: a*c - b*s with a = own, b = partner; hi: a*s + b*c with a = partner
-                    rope_y[i] = lo ? x[b][i] * rc[i] - pa * rs[i] : pa * rs[i] + x[b][i] * rc[i];
-                }
-#pragma unroll
-                for (int i = 0; i < E; i++) x[b][i] = rope_y[i];
-            } else if (kind[b] != 2) {
-                // Partial rotary: the partner of each pair comes from the
-                // wave's LDS row (LDS operations of one wave complete in order).
-#pragma unroll
-                for (int i = 0; i < E; i++) buf[wave][e0 + i] = x[b][i];
-                __builtin_amdgcn_wave_barrier();
-                float y[E];
-#pragma unroll
-                for (int i = 0; i < E; i++) {
-                    const int e = e0 + i;
-                    y[i] = x[b][i];
-                    if (e < rotary_dim) {
-                        if (neox) {
-                            const int j = e < half ? e : e - half;
-                            const float a = buf[wave][j], c = buf[wave][j + half];
-                            y[i] = e < half ? a * rc[i] - c * rs[i] : a * rs[i] + c * rc[i];
-                        } else {
-                            const float a = buf[wave][e & ~1], c = buf[wave][e | 1];
-                            y[i] = (e & 1) ? a * rs[i] + c * rc[i] : a * rc[i] - c * rs[i];
-                        }
-                    }
-                }
-                __builtin_amdgcn_wave_barrier();  // the row is rewritten by the next slot
-#pragma unroll
-                for (int i = 0; i < E; i++) x[b][i] = y[i];
-            }
-            if (kind[b] == 0)
-                store_e<QDT, E>(q_out, row * q_dim + (int64_t)head[b] * D + e0, x[b]);
-            else
-                store_e<KVDT, E>(kind[b] == 1 ? k_cache : v_cache,
-                                 (int64_t)pos * kv_stride + (int64_t)head[b] * D + e0, x[b]);
+            epi.norm_rope(x[b], kind[b], buf[wave]);
+            store_head<D, QDT, KVDT>(x[b], kind[b], head[b], row, pos, e0, q_dim, q_out, k_cache,
+                                     v_cache, kv_stride);
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Decode-side Q/K/V projection with the append fused into its epilogue
+// (crates/ullm-model/src/lib.rs:857-914; the Metal forward's wq/wk/wv
+// matvecs into q and the cache slot, bias, q/k norm and RoPE,
+// forward.rs:415-447): y = W x per head vector, W row-major [out][in_dim] in
+// f32, f16 or bf16 (math.rs:9-21 matvec_q: dequantised row times x, f32
+// sums), then the same head epilogue as qkv_append_kernel.
+//
+// A workgroup owns one head vector (slot) of one token row: its
+// kProjWaves waves each compute D/kProjWaves rows of W, every lane
+// accumulating 16-byte chunks of a row in f32 with x's matching chunk
+// (loaded once per chunk for all of the wave's rows), then a wave sum per
+// row.  The D results meet in LDS and wave 0 finishes the head.  The kernel
+// streams W once (HBM-bound); a CU pulls the D x in_dim slice of one head.
+constexpr int kProjWaves = 16;
+
+template <int WDT>
+struct WVec;
+template <> struct WVec<ULLM_DT_F32> { static constexpr int n = 4; };
+template <> struct WVec<ULLM_DT_F16> { static constexpr int n = 8; };
+template <> struct WVec<ULLM_DT_BF16> { static constexpr int n = 8; };
+
+// Widen one 16-byte chunk of W to f32.
+template <int WDT>
+__device__ __forceinline__ void widen_w(const u32x4 &r, float *o) {
+    if constexpr (WDT == ULLM_DT_F32) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = __uint_as_float(r[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if constexpr (WDT == ULLM_DT_BF16) { o[2 * i] = bf16_lo(r[i]); o[2 * i + 1] = bf16_hi(r[i]); }
+            else { o[2 * i] = f16_lo(r[i]); o[2 * i + 1] = f16_hi(r[i]); }
+        }
+    }
+}
+
+template <int D, int WDT, int QDT, int KVDT>
+__global__ __launch_bounds__(kProjWaves * 64) void qkv_proj_kernel(
+    const float *__restrict__ x, int in_dim, const char *__restrict__ wq,
+    const char *__restrict__ wk, const char *__restrict__ wv, const float *__restrict__ q_bias,
+    const float *__restrict__ k_bias, const float *__restrict__ v_bias,
+    const float *__restrict__ q_norm, const float *__restrict__ k_norm, float eps,
+    const float *__restrict__ cs, int neox, int rotary_dim, int start_pos, int n_head,
+    int n_kv_head, void *q_out, void *k_cache, void *v_cache, int64_t kv_stride) {
+    constexpr int E = D / 64, RPW = D / kProjWaves, VEC = WVec<WDT>::n;
+    constexpr int WB = WDT == ULLM_DT_F32 ? 4 : 2;  // bytes per weight
+    __shared__ float ys[D];
+    __shared__ float lrow[D];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slot = blockIdx.x, row = blockIdx.y;
+    const int kind = slot < n_head ? 0 : (slot < n_head + n_kv_head ? 1 : 2);
+    const int head = kind == 0 ? slot : (kind == 1 ? slot - n_head : slot - n_head - n_kv_head);
+    const char *w = (kind == 0 ? wq : (kind == 1 ? wk : wv)) +
+                    ((int64_t)head * D + wave * RPW) * in_dim * WB;
+    const float *xr = x + (int64_t)row * in_dim;
+
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) acc[r] = 0.f;
+    // Software pipeline over 16-byte chunks of the rows: chunk i+1's loads
+    // are in flight while chunk i is multiplied (chunks past in_dim read 0).
+    auto load = [&](int c, u32x4 (&wr)[RPW], float (&xv)[VEC]) {
+        const bool ok = c < in_dim;
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+            wr[r] = ok ? *(const u32x4 *)(w + ((int64_t)r * in_dim + c) * WB) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int h = 0; h < VEC / 4; h++) {
+            const float4 t = ok ? *(const float4 *)(xr + c + 4 * h) : float4{0.f, 0.f, 0.f, 0.f};
+            xv[4 * h] = t.x; xv[4 * h + 1] = t.y; xv[4 * h + 2] = t.z; xv[4 * h + 3] = t.w;
+        }
+    };
+    auto mac = [&](const u32x4 (&wr)[RPW], const float (&xv)[VEC]) {
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            float wf[VEC];
+            widen_w<WDT>(wr[r], wf);
+#pragma unroll
+            for (int i = 0; i < VEC; i++) acc[r] = __builtin_fmaf(wf[i], xv[i], acc[r]);
+        }
+    };
+    constexpr int STEP = 64 * VEC;
+    u32x4 wa[RPW], wb[RPW];
+    float xa[VEC], xb[VEC];
+    int c = lane * VEC;
+    load(c, wa, xa);
+    for (; c < in_dim; c += 2 * STEP) {
+        load(c + STEP, wb, xb);
+        mac(wa, xa);
+        if (c + STEP >= in_dim) break;
+        load(c + 2 * STEP, wa, xa);
+        mac(wb, xb);
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const float t = wave_sum(acc[r]);
+        if (lane == 0) ys[wave * RPW + r] = t;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    const int pos = start_pos + row;
+    const HeadEpi<D> epi(cs, pos, rotary_dim, neox, q_norm, k_norm, eps);
+    float v[E];
+    load_e<E>(ys + epi.e0, v);
+    const float *bias = kind == 0 ? q_bias : (kind == 1 ? k_bias : v_bias);
+    if (bias) {
+        float bv[E];
+        load_e<E>(bias + (int64_t)head * D + epi.e0, bv);
+#pragma unroll
+        for (int i = 0; i < E; i++) v[i] += bv[i];
+    }
+    epi.norm_rope(v, kind, lrow);
+    store_head<D, QDT, KVDT>(v, kind, head, row, pos, epi.e0, (int64_t)n_head * D, q_out,
+                             k_cache, v_cache, kv_stride);
 }
 
 template <int D, int QDT>
@@ -272,4 +415,89 @@ extern "C" int ullm_hip_qkv_append(const float *q_in, const float *k_in, const f
         default: launch_q<256>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride); break;
     }
     return check_hip(hipGetLastError(), "qkv_append launch");
+}
+
+namespace ullm {
+
+template <int D, int WDT, int QDT>
+static void launch_proj_kv(int kvdt, dim3 g, hipStream_t st, const float *x, int in_dim,
+                           const char *wq, const char *wk, const char *wv, const float *qb,
+                           const float *kb, const float *vb, const float *qn, const float *kn,
+                           float eps, const float *cs, int neox, int rd, int sp, int nh, int nkv,
+                           void *qo, void *kc, void *vc, int64_t kvs) {
+#define ULLM_PROJ(KV) hipLaunchKernelGGL((qkv_proj_kernel<D, WDT, QDT, KV>), g, dim3(kProjWaves * 64), 0, st, \
+                                         x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs)
+    if (kvdt == ULLM_DT_F32) ULLM_PROJ(ULLM_DT_F32);
+    else if (kvdt == ULLM_DT_F16) ULLM_PROJ(ULLM_DT_F16);
+    else ULLM_PROJ(ULLM_DT_BF16);
+#undef ULLM_PROJ
+}
+
+template <int D, int WDT>
+static void launch_proj_q(int qdt, int kvdt, dim3 g, hipStream_t st, const float *x, int in_dim,
+                          const char *wq, const char *wk, const char *wv, const float *qb,
+                          const float *kb, const float *vb, const float *qn, const float *kn,
+                          float eps, const float *cs, int neox, int rd, int sp, int nh, int nkv,
+                          void *qo, void *kc, void *vc, int64_t kvs) {
+    if (qdt == ULLM_DT_F32) launch_proj_kv<D, WDT, ULLM_DT_F32>(kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
+    else if (qdt == ULLM_DT_F16) launch_proj_kv<D, WDT, ULLM_DT_F16>(kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
+    else launch_proj_kv<D, WDT, ULLM_DT_BF16>(kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
+}
+
+template <int D>
+static void launch_proj_w(int wdt, int qdt, int kvdt, dim3 g, hipStream_t st, const float *x,
+                          int in_dim, const char *wq, const char *wk, const char *wv,
+                          const float *qb, const float *kb, const float *vb, const float *qn,
+                          const float *kn, float eps, const float *cs, int neox, int rd, int sp,
+                          int nh, int nkv, void *qo, void *kc, void *vc, int64_t kvs) {
+    if (wdt == ULLM_DT_F32) launch_proj_q<D, ULLM_DT_F32>(qdt, kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
+    else if (wdt == ULLM_DT_F16) launch_proj_q<D, ULLM_DT_F16>(qdt, kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
+    else launch_proj_q<D, ULLM_DT_BF16>(qdt, kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
+}
+
+}  // namespace ullm
+
+extern "C" int ullm_hip_qkv_proj_append(const float *x, int in_dim, const void *w_q,
+                                        const void *w_k, const void *w_v, int w_dtype,
+                                        const float *q_bias, const float *k_bias,
+                                        const float *v_bias, const float *q_norm,
+                                        const float *k_norm, float eps, const float *rope_cs,
+                                        int rope_n_pos, int rope_neox, int rotary_dim, int rows,
+                                        int start_pos, int n_head, int n_kv_head, int head_dim,
+                                        void *q_out, int q_dtype, void *k_cache, void *v_cache,
+                                        int kv_dtype, int64_t kv_stride, void *stream) {
+    if (!dtype_ok(w_dtype) || !dtype_ok(q_dtype) || !dtype_ok(kv_dtype))
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "qkv_proj_append: dtype w=%d q=%d kv=%d",
+                         w_dtype, q_dtype, kv_dtype);
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "qkv_proj_append: head_dim %d not in {64,128,256}",
+                         head_dim);
+    if (rows < 0 || start_pos < 0 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_proj_append: bad rows/heads");
+    if (in_dim < 8 || in_dim % 8)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_proj_append: in_dim %d must be a positive multiple of 8",
+                         in_dim);
+    if (rotary_dim < 2 || rotary_dim > head_dim || (rotary_dim & 1))
+        return set_error(ULLM_HIP_E_INVALID, "qkv_proj_append: rotary_dim %d", rotary_dim);
+    if (kv_stride < (int64_t)n_kv_head * head_dim)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_proj_append: kv_stride too small");
+    if (rows == 0) return ULLM_HIP_OK;
+    if (!x || !w_q || !w_k || !w_v || !rope_cs || !q_out || !k_cache || !v_cache)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_proj_append: null tensor pointer");
+    if (((uintptr_t)x | (uintptr_t)w_q | (uintptr_t)w_k | (uintptr_t)w_v) & 15)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_proj_append: x and weights must be 16-byte aligned");
+    if (rope_n_pos < start_pos + rows)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_proj_append: rope table has %d positions, need %d",
+                         rope_n_pos, start_pos + rows);
+    if (rows > 65535)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_proj_append: rows %d > 65535", rows);
+    dim3 grid((unsigned)(n_head + 2 * n_kv_head), (unsigned)rows);
+    hipStream_t st = (hipStream_t)stream;
+    const char *wq = (const char *)w_q, *wk = (const char *)w_k, *wv = (const char *)w_v;
+    switch (head_dim) {
+        case 64: launch_proj_w<64>(w_dtype, q_dtype, kv_dtype, grid, st, x, in_dim, wq, wk, wv, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride); break;
+        case 128: launch_proj_w<128>(w_dtype, q_dtype, kv_dtype, grid, st, x, in_dim, wq, wk, wv, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride); break;
+        default: launch_proj_w<256>(w_dtype, q_dtype, kv_dtype, grid, st, x, in_dim, wq, wk, wv, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride); break;
+    }
+    return check_hip(hipGetLastError(), "qkv_proj_append launch");
 }
