@@ -141,7 +141,12 @@ int ullm_hip_qkv_append(const float *q_in, const float *k_in, const float *v_in,
  * w_q: [n_head*head_dim][in_dim], w_k / w_v: [n_kv_head*head_dim][in_dim],
  *      row-major, w_dtype f32, f16 or bf16 (other weight formats: unsupported)
  * in_dim a multiple of 8; x and the weights 16-byte aligned; rows <= 65535.
- * One workgroup per (head vector, row): HBM-bound on the weights. */
+ * HBM-bound on the weights.  With few head vectors (rows * (n_head +
+ * 2*n_kv_head) < 256, i.e. decode) each is split over 4 workgroups that
+ * meet in `workspace`: size it with ullm_hip_qkv_proj_workspace_bytes and
+ * ZERO it once after allocating it (its counters return to zero after every
+ * call); calls sharing a workspace must not overlap.  With more head vectors
+ * the workspace is not used (0 bytes needed; may be NULL). */
 int ullm_hip_qkv_proj_append(const float *x, int in_dim, const void *w_q, const void *w_k,
                              const void *w_v, int w_dtype, const float *q_bias,
                              const float *k_bias, const float *v_bias, const float *q_norm,
@@ -149,7 +154,12 @@ int ullm_hip_qkv_proj_append(const float *x, int in_dim, const void *w_q, const 
                              int rope_n_pos, int rope_neox, int rotary_dim, int rows,
                              int start_pos, int n_head, int n_kv_head, int head_dim, void *q_out,
                              int q_dtype, void *k_cache, void *v_cache, int kv_dtype,
-                             int64_t kv_stride, void *stream);
+                             int64_t kv_stride, void *workspace, size_t workspace_bytes,
+                             void *stream);
+
+/* Workspace bytes ullm_hip_qkv_proj_append needs for this many rows (0 when
+ * it does not split head vectors). */
+size_t ullm_hip_qkv_proj_workspace_bytes(int rows, int n_head, int n_kv_head, int head_dim);
 
 #ifdef __cplusplus
 }

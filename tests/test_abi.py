@@ -104,7 +104,7 @@ def test_proj_append_validation():
         a = dict(x=None, in_dim=1536, wq=None, wk=None, wv=None, wdt=L.DT_BF16, qb=None, kb=None,
                  vb=None, qn=None, kn=None, eps=1e-6, cs=None, npos=10, neox=1, rd=128, rows=1,
                  sp=0, h=12, hk=2, d=128, qo=None, qdt=L.DT_F32, kc=None, vc=None,
-                 kvdt=L.DT_F16, kvs=256, st=None)
+                 kvdt=L.DT_F16, kvs=256, ws=None, wsb=0, st=None)
         a.update(kw)
         return f(*a.values())
 
@@ -116,3 +116,6 @@ def test_proj_append_validation():
     assert call(kvs=100) == L.E_INVALID
     assert call(rows=0) == L.OK  # nothing to do
     assert call() == L.E_INVALID  # null pointers
+    wsz = L.lib().ullm_hip_qkv_proj_workspace_bytes
+    assert wsz(1, 32, 8, 128) == 48 * 128 * 4 + 256  # decode: split, y + counters
+    assert wsz(2048, 32, 8, 128) == 0  # prefill rows: no split

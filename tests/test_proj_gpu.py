@@ -93,3 +93,18 @@ def test_weight_dtypes_head_dims(dev, wdt, D):
 def test_interleaved_and_partial_rotary(dev, neox):
     run_case(dev, 3, 10, 4, 2, 128, 264, "f16", 64, neox, norm=False, bias=False, qdt="bf16",
              kvdt="bf16", theta=1e4, seed=5)
+
+
+def test_many_rows_unsplit(dev):
+    """rows * head vectors >= 256: one workgroup per head vector, no workspace."""
+    assert A.proj_workspace(20, 8, 4, 128) is None
+    run_case(dev, 20, 3, 8, 4, 128, 384, "bf16", 128, True, norm=True, bias=True, qdt="bf16",
+             kvdt="bf16", seed=6)
+
+
+def test_split_counters_reset_between_calls(dev):
+    """The split path's arrival counters return to zero: three calls in a row on
+    one workspace (different inputs) all match the oracle."""
+    for seed in (7, 8, 9):
+        run_case(dev, 1, 100, 12, 2, 128, 1536, "bf16", 128, True, norm=True, bias=False,
+                 qdt="f32", kvdt="bf16", seed=seed)

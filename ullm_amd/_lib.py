@@ -35,8 +35,9 @@ SIGNATURES = {
     "ullm_hip_qkv_proj_append": (
         _i,
         [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _i, _i, _i,
-         _i, _i, _vp, _i, _vp, _vp, _i, _i64, _vp],
+         _i, _i, _vp, _i, _vp, _vp, _i, _i64, _vp, _sz, _vp],
     ),
+    "ullm_hip_qkv_proj_workspace_bytes": (_sz, [_i, _i, _i, _i]),
 }
 
 

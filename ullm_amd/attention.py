@@ -147,13 +147,30 @@ def qkv_append(q, k, v, k_cache, v_cache, rope_cs, *, start_pos, n_head, n_kv_he
     return q_out
 
 
+_proj_ws = {}
+
+
+def proj_workspace(rows, n_head, n_kv_head, head_dim, device="cuda"):
+    """The (zeroed once, reusable) workspace ullm_hip_qkv_proj_append needs for
+    this shape, or None; cached per shape and device."""
+    n = int(L.lib().ullm_hip_qkv_proj_workspace_bytes(rows, n_head, n_kv_head, head_dim))
+    if n == 0:
+        return None
+    key = (str(torch.device(device)), rows, n_head, n_kv_head, head_dim)
+    if key not in _proj_ws:
+        _proj_ws[key] = torch.zeros(n, dtype=torch.uint8, device=device)
+    return _proj_ws[key]
+
+
 def qkv_proj_append(x, w_q, w_k, w_v, k_cache, v_cache, rope_cs, *, start_pos, n_head,
                     n_kv_head, head_dim, rotary_dim=None, neox=True, q_norm=None, k_norm=None,
                     eps=1e-6, q_bias=None, k_bias=None, v_bias=None, q_out=None, q_dtype=None,
-                    kv_stride=None, stream=None):
+                    kv_stride=None, workspace=None, stream=None):
     """Q/K/V projection (matvec_q, math.rs:9-21) with the append fused in
     (lib.rs:857-914).  x: [rows, in_dim] f32; w_*: [out, in_dim] f32/f16/bf16.
-    Returns q_out ([rows, n_head*D], q_dtype); K/V land in the cache."""
+    Returns q_out ([rows, n_head*D], q_dtype); K/V land in the cache.  The
+    workspace defaults to a cached one per shape (one caller at a time, as for
+    GpuForward)."""
     rows, in_dim = x.shape
     _need_cuda(x, w_q, w_k, w_v, k_cache, v_cache, rope_cs)
     if x.dtype != torch.float32 or not x.is_contiguous():
@@ -171,11 +188,15 @@ def qkv_proj_append(x, w_q, w_k, w_v, k_cache, v_cache, rope_cs, *, start_pos, n
         q_out = torch.empty(rows, n_head * head_dim, dtype=q_dtype, device=x.device)
     if kv_stride is None:
         kv_stride = n_kv_head * head_dim
+    if workspace is None:
+        workspace = proj_workspace(rows, n_head, n_kv_head, head_dim, x.device)
+    wsb = 0 if workspace is None else workspace.numel() * workspace.element_size()
     rc = L.lib().ullm_hip_qkv_proj_append(
         _ptr(x), in_dim, _ptr(w_q), _ptr(w_k), _ptr(w_v), _dt(w_q), _ptr(q_bias), _ptr(k_bias),
         _ptr(v_bias), _ptr(q_norm), _ptr(k_norm), float(eps), _ptr(rope_cs), rope_cs.shape[0],
         int(bool(neox)), rotary_dim, rows, start_pos, n_head, n_kv_head, head_dim, _ptr(q_out),
-        _DT[q_out.dtype], _ptr(k_cache), _ptr(v_cache), _dt(k_cache), kv_stride, _stream(stream))
+        _DT[q_out.dtype], _ptr(k_cache), _ptr(v_cache), _dt(k_cache), kv_stride, _ptr(workspace),
+        wsb, _stream(stream))
     L.check(rc)
     return q_out
 

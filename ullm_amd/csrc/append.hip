@@ -18,6 +18,7 @@
 // (forward.rs:416-447, :799-853; shader.metal:828-941) with one launch.
 #include <cmath>
 #include "common.hpp"
+#include "mfma_util.hpp"
 #include "wave.hpp"
 
 namespace ullm {
@@ -248,25 +249,29 @@ __device__ __forceinline__ void widen_w(const u32x4 &r, float *o) {
     }
 }
 
-template <int D, int WDT, int QDT, int KVDT>
+template <int D, int WDT, int QDT, int KVDT, int NSP>
 __global__ __launch_bounds__(kProjWaves * 64) void qkv_proj_kernel(
     const float *__restrict__ x, int in_dim, const char *__restrict__ wq,
     const char *__restrict__ wk, const char *__restrict__ wv, const float *__restrict__ q_bias,
     const float *__restrict__ k_bias, const float *__restrict__ v_bias,
     const float *__restrict__ q_norm, const float *__restrict__ k_norm, float eps,
     const float *__restrict__ cs, int neox, int rotary_dim, int start_pos, int n_head,
-    int n_kv_head, void *q_out, void *k_cache, void *v_cache, int64_t kv_stride) {
-    constexpr int E = D / 64, RPW = D / kProjWaves, VEC = WVec<WDT>::n;
+    int n_kv_head, void *q_out, void *k_cache, void *v_cache, int64_t kv_stride,
+    float *__restrict__ ws_y, uint32_t *__restrict__ ws_cnt) {
+    constexpr int E = D / 64, RPW = D / kProjWaves / NSP, VEC = WVec<WDT>::n;
     constexpr int WB = WDT == ULLM_DT_F32 ? 4 : 2;  // bytes per weight
+    static_assert(RPW >= 1, "rows per wave");
     __shared__ float ys[D];
     __shared__ float lrow[D];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int slot = blockIdx.x, row = blockIdx.y;
+    const int slot = blockIdx.x / NSP, part = blockIdx.x % NSP, row = blockIdx.y;
+    const int slots = n_head + 2 * n_kv_head;
     const int kind = slot < n_head ? 0 : (slot < n_head + n_kv_head ? 1 : 2);
     const int head = kind == 0 ? slot : (kind == 1 ? slot - n_head : slot - n_head - n_kv_head);
+    const int r0 = part * (D / NSP) + wave * RPW;  // first W row of this wave in the head
     const char *w = (kind == 0 ? wq : (kind == 1 ? wk : wv)) +
-                    ((int64_t)head * D + wave * RPW) * in_dim * WB;
+                    ((int64_t)head * D + r0) * in_dim * WB;
     const float *xr = x + (int64_t)row * in_dim;
 
     float acc[RPW];
@@ -309,10 +314,31 @@ __global__ __launch_bounds__(kProjWaves * 64) void qkv_proj_kernel(
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
         const float t = wave_sum(acc[r]);
-        if (lane == 0) ys[wave * RPW + r] = t;
+        if (lane == 0) ys[r0 + r] = t;
     }
     __syncthreads();
     if (wave != 0) return;
+    if constexpr (NSP > 1) {
+        // NSP workgroups share a head vector: wave 0 of each stores its part
+        // to the workspace and counts itself in (agent-scope acquire-release:
+        // the wait for the wave's stores and the L2 write-back come with the
+        // release); the last to arrive reads the whole vector back, finishes
+        // the head and resets the counter for the next call.
+        constexpr int PART = D / NSP;
+        float *yh = ws_y + ((int64_t)row * slots + slot) * D;
+        for (int i = lane; i < PART; i += 64) yh[part * PART + i] = ys[part * PART + i];
+        uint32_t prev = 0;
+        if (lane == 0) {
+            uint32_t *cnt = ws_cnt + (int64_t)row * slots + slot;
+            prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            if (prev == NSP - 1) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        prev = __builtin_amdgcn_readfirstlane(prev);
+        if (prev != NSP - 1) return;
+        for (int i = lane; i < D; i += 64)
+            ys[i] = __hip_atomic_load(yh + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_wave_barrier();
+    }
     const int pos = start_pos + row;
     const HeadEpi<D> epi(cs, pos, rotary_dim, neox, q_norm, k_norm, eps);
     float v[E];
@@ -419,40 +445,67 @@ extern "C" int ullm_hip_qkv_append(const float *q_in, const float *k_in, const f
 
 namespace ullm {
 
+// A head vector is split over kProjSplit workgroups when the grid would
+// otherwise leave most CUs idle (decode: a few dozen head vectors).
+constexpr int kProjSplit = 4;
+constexpr int kProjSplitBelow = 256;  // rows * slots under which to split
+
+static bool proj_split(int rows, int slots) { return (int64_t)rows * slots < kProjSplitBelow; }
+
+struct ProjArgs {
+    const float *x;
+    int in_dim;
+    const char *wq, *wk, *wv;
+    const float *qb, *kb, *vb, *qn, *kn;
+    float eps;
+    const float *cs;
+    int neox, rd, sp, nh, nkv;
+    void *qo, *kc, *vc;
+    int64_t kvs;
+    float *ws_y;
+    uint32_t *ws_cnt;
+};
+
+template <int D, int WDT, int QDT, int KVDT>
+static void launch_proj(bool split, int rows, hipStream_t st, const ProjArgs &a) {
+    const int slots = a.nh + 2 * a.nkv;
+    auto go = [&](auto nspc) {
+        constexpr int NSP = decltype(nspc)::value;
+        hipLaunchKernelGGL((qkv_proj_kernel<D, WDT, QDT, KVDT, NSP>),
+                           dim3((unsigned)(slots * NSP), (unsigned)rows), dim3(kProjWaves * 64), 0, st,
+                           a.x, a.in_dim, a.wq, a.wk, a.wv, a.qb, a.kb, a.vb, a.qn, a.kn, a.eps, a.cs,
+                           a.neox, a.rd, a.sp, a.nh, a.nkv, a.qo, a.kc, a.vc, a.kvs, a.ws_y, a.ws_cnt);
+    };
+    if (split) go(Int<kProjSplit>{});
+    else go(Int<1>{});
+}
+
 template <int D, int WDT, int QDT>
-static void launch_proj_kv(int kvdt, dim3 g, hipStream_t st, const float *x, int in_dim,
-                           const char *wq, const char *wk, const char *wv, const float *qb,
-                           const float *kb, const float *vb, const float *qn, const float *kn,
-                           float eps, const float *cs, int neox, int rd, int sp, int nh, int nkv,
-                           void *qo, void *kc, void *vc, int64_t kvs) {
-#define ULLM_PROJ(KV) hipLaunchKernelGGL((qkv_proj_kernel<D, WDT, QDT, KV>), g, dim3(kProjWaves * 64), 0, st, \
-                                         x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs)
-    if (kvdt == ULLM_DT_F32) ULLM_PROJ(ULLM_DT_F32);
-    else if (kvdt == ULLM_DT_F16) ULLM_PROJ(ULLM_DT_F16);
-    else ULLM_PROJ(ULLM_DT_BF16);
-#undef ULLM_PROJ
+static void launch_proj_kv(int kvdt, bool split, int rows, hipStream_t st, const ProjArgs &a) {
+    if (kvdt == ULLM_DT_F32) launch_proj<D, WDT, QDT, ULLM_DT_F32>(split, rows, st, a);
+    else if (kvdt == ULLM_DT_F16) launch_proj<D, WDT, QDT, ULLM_DT_F16>(split, rows, st, a);
+    else launch_proj<D, WDT, QDT, ULLM_DT_BF16>(split, rows, st, a);
 }
 
 template <int D, int WDT>
-static void launch_proj_q(int qdt, int kvdt, dim3 g, hipStream_t st, const float *x, int in_dim,
-                          const char *wq, const char *wk, const char *wv, const float *qb,
-                          const float *kb, const float *vb, const float *qn, const float *kn,
-                          float eps, const float *cs, int neox, int rd, int sp, int nh, int nkv,
-                          void *qo, void *kc, void *vc, int64_t kvs) {
-    if (qdt == ULLM_DT_F32) launch_proj_kv<D, WDT, ULLM_DT_F32>(kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
-    else if (qdt == ULLM_DT_F16) launch_proj_kv<D, WDT, ULLM_DT_F16>(kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
-    else launch_proj_kv<D, WDT, ULLM_DT_BF16>(kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
+static void launch_proj_q(int qdt, int kvdt, bool split, int rows, hipStream_t st, const ProjArgs &a) {
+    if (qdt == ULLM_DT_F32) launch_proj_kv<D, WDT, ULLM_DT_F32>(kvdt, split, rows, st, a);
+    else if (qdt == ULLM_DT_F16) launch_proj_kv<D, WDT, ULLM_DT_F16>(kvdt, split, rows, st, a);
+    else launch_proj_kv<D, WDT, ULLM_DT_BF16>(kvdt, split, rows, st, a);
 }
 
 template <int D>
-static void launch_proj_w(int wdt, int qdt, int kvdt, dim3 g, hipStream_t st, const float *x,
-                          int in_dim, const char *wq, const char *wk, const char *wv,
-                          const float *qb, const float *kb, const float *vb, const float *qn,
-                          const float *kn, float eps, const float *cs, int neox, int rd, int sp,
-                          int nh, int nkv, void *qo, void *kc, void *vc, int64_t kvs) {
-    if (wdt == ULLM_DT_F32) launch_proj_q<D, ULLM_DT_F32>(qdt, kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
-    else if (wdt == ULLM_DT_F16) launch_proj_q<D, ULLM_DT_F16>(qdt, kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
-    else launch_proj_q<D, ULLM_DT_BF16>(qdt, kvdt, g, st, x, in_dim, wq, wk, wv, qb, kb, vb, qn, kn, eps, cs, neox, rd, sp, nh, nkv, qo, kc, vc, kvs);
+static void launch_proj_w(int wdt, int qdt, int kvdt, bool split, int rows, hipStream_t st,
+                          const ProjArgs &a) {
+    if (wdt == ULLM_DT_F32) launch_proj_q<D, ULLM_DT_F32>(qdt, kvdt, split, rows, st, a);
+    else if (wdt == ULLM_DT_F16) launch_proj_q<D, ULLM_DT_F16>(qdt, kvdt, split, rows, st, a);
+    else launch_proj_q<D, ULLM_DT_BF16>(qdt, kvdt, split, rows, st, a);
+}
+
+static size_t proj_ws_bytes(int rows, int slots, int D) {
+    if (!proj_split(rows, slots)) return 0;
+    const size_t n = (size_t)rows * slots;
+    return n * D * 4 + (n * 4 + 255) / 256 * 256;
 }
 
 }  // namespace ullm
@@ -465,7 +518,8 @@ extern "C" int ullm_hip_qkv_proj_append(const float *x, int in_dim, const void *
                                         int rope_n_pos, int rope_neox, int rotary_dim, int rows,
                                         int start_pos, int n_head, int n_kv_head, int head_dim,
                                         void *q_out, int q_dtype, void *k_cache, void *v_cache,
-                                        int kv_dtype, int64_t kv_stride, void *stream) {
+                                        int kv_dtype, int64_t kv_stride, void *workspace,
+                                        size_t workspace_bytes, void *stream) {
     if (!dtype_ok(w_dtype) || !dtype_ok(q_dtype) || !dtype_ok(kv_dtype))
         return set_error(ULLM_HIP_E_UNSUPPORTED, "qkv_proj_append: dtype w=%d q=%d kv=%d",
                          w_dtype, q_dtype, kv_dtype);
@@ -491,13 +545,28 @@ extern "C" int ullm_hip_qkv_proj_append(const float *x, int in_dim, const void *
                          rope_n_pos, start_pos + rows);
     if (rows > 65535)
         return set_error(ULLM_HIP_E_INVALID, "qkv_proj_append: rows %d > 65535", rows);
-    dim3 grid((unsigned)(n_head + 2 * n_kv_head), (unsigned)rows);
+    const int slots = n_head + 2 * n_kv_head;
+    const bool split = proj_split(rows, slots);
+    const size_t need = proj_ws_bytes(rows, slots, head_dim);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return set_error(ULLM_HIP_E_WORKSPACE, "qkv_proj_append: workspace of %zu bytes needed, %zu given",
+                         need, workspace_bytes);
+    ProjArgs a{x, in_dim, (const char *)w_q, (const char *)w_k, (const char *)w_v, q_bias, k_bias,
+               v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, start_pos, n_head,
+               n_kv_head, q_out, k_cache, v_cache, kv_stride,
+               split ? (float *)workspace : nullptr,
+               split ? (uint32_t *)((char *)workspace + (size_t)rows * slots * head_dim * 4) : nullptr};
     hipStream_t st = (hipStream_t)stream;
-    const char *wq = (const char *)w_q, *wk = (const char *)w_k, *wv = (const char *)w_v;
     switch (head_dim) {
-        case 64: launch_proj_w<64>(w_dtype, q_dtype, kv_dtype, grid, st, x, in_dim, wq, wk, wv, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride); break;
-        case 128: launch_proj_w<128>(w_dtype, q_dtype, kv_dtype, grid, st, x, in_dim, wq, wk, wv, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride); break;
-        default: launch_proj_w<256>(w_dtype, q_dtype, kv_dtype, grid, st, x, in_dim, wq, wk, wv, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride); break;
+        case 64: launch_proj_w<64>(w_dtype, q_dtype, kv_dtype, split, rows, st, a); break;
+        case 128: launch_proj_w<128>(w_dtype, q_dtype, kv_dtype, split, rows, st, a); break;
+        default: launch_proj_w<256>(w_dtype, q_dtype, kv_dtype, split, rows, st, a); break;
     }
     return check_hip(hipGetLastError(), "qkv_proj_append launch");
+}
+
+extern "C" size_t ullm_hip_qkv_proj_workspace_bytes(int rows, int n_head, int n_kv_head,
+                                                    int head_dim) {
+    if (rows < 1 || n_head < 1 || n_kv_head < 1 || head_dim < 1) return 0;
+    return proj_ws_bytes(rows, n_head + 2 * n_kv_head, head_dim);
 }
