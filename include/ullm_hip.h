@@ -161,6 +161,20 @@ int ullm_hip_qkv_proj_append(const float *x, int in_dim, const void *w_q, const 
  * it does not split head vectors). */
 size_t ullm_hip_qkv_proj_workspace_bytes(int rows, int n_head, int n_kv_head, int head_dim);
 
+/* Batched projection for prefill: y[s*out_dim + o] = sum_i w[o*in_dim + i] *
+ * x[s*in_dim + i] for s < n_cols, o < out_dim.  Replaces the reference's
+ * batched matmul (crates/ullm-metal/src/forward.rs:675-726, kernel
+ * matmul_bf16_tiled at shader.metal:519-566), same argument meaning: w is
+ * [out_dim, in_dim] row-major, x [n_cols, in_dim] and y [n_cols, out_dim]
+ * token-major f32; the caller offsets y (y_off) as forward.rs does when K/V
+ * land in the cache.  Weights bf16 only (w_dtype = ULLM_DT_BF16, as the
+ * reference's batched path; other dtypes -> ULLM_HIP_E_UNSUPPORTED).  The
+ * activations enter the matrix cores as a bf16 hi + lo pair (16 significant
+ * bits), accumulation is f32.  in_dim % 8 == 0, out_dim % 4 == 0, w/x/y
+ * 16-byte aligned, weight below 2 GiB.  n_cols == 0 is a no-op. */
+int ullm_hip_matmul(const void *w, int w_dtype, const float *x, float *y, int in_dim,
+                    int out_dim, int n_cols, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -119,3 +119,21 @@ def test_proj_append_validation():
     wsz = L.lib().ullm_hip_qkv_proj_workspace_bytes
     assert wsz(1, 32, 8, 128) == 48 * 128 * 4 + 256  # decode: split, y + counters
     assert wsz(2048, 32, 8, 128) == 0  # prefill rows: no split
+
+
+def test_matmul_validation():
+    f = L.lib().ullm_hip_matmul
+
+    def call(**kw):
+        a = dict(w=None, wdt=L.DT_BF16, x=None, y=None, i=2560, o=4096, n=16, st=None)
+        a.update(kw)
+        return f(*a.values())
+
+    assert call(wdt=L.DT_F32) == L.E_UNSUPPORTED  # batched path is bf16, as forward.rs:710-714
+    assert call(wdt=L.DT_F16) == L.E_UNSUPPORTED
+    assert call(i=2564) == L.E_INVALID  # in_dim % 8
+    assert call(o=4098) == L.E_INVALID  # out_dim % 4
+    assert call(n=-1) == L.E_INVALID
+    assert call(i=1 << 20, o=1 << 11) == L.E_INVALID  # 4 GiB weight
+    assert call(n=0) == L.OK  # nothing to do
+    assert call() == L.E_INVALID  # null pointers

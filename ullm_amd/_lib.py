@@ -38,6 +38,7 @@ SIGNATURES = {
          _i, _i, _vp, _i, _vp, _vp, _i, _i64, _vp, _sz, _vp],
     ),
     "ullm_hip_qkv_proj_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "ullm_hip_matmul": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp]),
 }
 
 

@@ -201,6 +201,26 @@ def qkv_proj_append(x, w_q, w_k, w_v, k_cache, v_cache, rope_cs, *, start_pos, n
     return q_out
 
 
+def matmul(w, x, y=None, *, stream=None):
+    """Batched projection y = x . w^T (forward.rs:675-726, shader.metal:519-566).
+    w: [out, in] bf16; x: [n_cols, in] f32; y: [n_cols, out] f32 (allocated if
+    None, else written in place, e.g. a view into an f32 KV cache)."""
+    _need_cuda(w, x)
+    if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+        raise L.UllmHipError(L.E_INVALID, f"shapes w {tuple(w.shape)} x {tuple(x.shape)}")
+    if x.dtype != torch.float32 or not x.is_contiguous() or not w.is_contiguous():
+        raise L.UllmHipError(L.E_INVALID, "x must be contiguous f32 and w contiguous")
+    n_cols, in_dim = x.shape
+    out_dim = w.shape[0]
+    if y is None:
+        y = torch.empty(n_cols, out_dim, dtype=torch.float32, device=x.device)
+    elif y.dtype != torch.float32 or tuple(y.shape) != (n_cols, out_dim) or not y.is_contiguous():
+        raise L.UllmHipError(L.E_INVALID, "y must be contiguous f32 [n_cols, out]")
+    L.check(L.lib().ullm_hip_matmul(_ptr(w), _dt(w), _ptr(x), _ptr(y), in_dim, out_dim, n_cols,
+                                    _stream(stream)))
+    return y
+
+
 @dataclass
 class AttnParams:
     """The attention fields of the reference's GpuParams (forward.rs:23-51)."""

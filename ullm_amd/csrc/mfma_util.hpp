@@ -86,6 +86,11 @@ typedef __attribute__((address_space(3))) void lds_void;
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char *dst, int voff, int soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, voff, soff, 0, 2);
 }
+// Same load with the default cache policy, for operands that other
+// workgroups re-read from L2 (GEMM tiles).
+__device__ __forceinline__ void dma16_cached(__amdgpu_buffer_rsrc_t r, char *dst, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, voff, soff, 0, 0);
+}
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
 }
