@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "append", "proj", "matmul", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "append", "proj", "matmul", "paged", "copy"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     return ap.parse_args()
 
@@ -272,6 +272,93 @@ def bench_matmul(torch, A, args, S, hidden, outs):
     return dict(us=us, flop=flop, tflops=flop / (us * 1e6))
 
 
+def bench_paged(torch, A, args, H, Hk, D, B, lo, hi, n_layer, page, dt):
+    """cfg5 batch 8: independent sequences with ragged lengths in [lo, hi]
+    (SplitMix64), 48 layers per step, over a paged cache (page positions per
+    page, pages of a layer shuffled over its pool) and, for comparison, over
+    the contiguous layout ullm_hip_attn_decode takes.  Layer l reads pool
+    l % 4: consecutive layers never share data, and 4 pools exceed the MALL.
+    Algorithmic bytes per layer = sum(len) x 2 x Hk x D x 2."""
+    import numpy as np
+
+    from ullm_amd import synth
+    dev = torch.device("cuda")
+    lens = synth.ragged_lengths(5, B, lo, hi)
+    L_ = max(lens)
+    kvs = Hk * D
+    need = [(n + page - 1) // page for n in lens]
+    n_pages = sum(need)
+    stride = (L_ + page - 1) // page
+    n_pool = 4
+    g = torch.Generator(device=dev).manual_seed(21)
+    rng = np.random.default_rng(21)
+    pools, tables = [], []
+    for _ in range(n_pool):
+        kp = torch.randn(n_pages, page, kvs, generator=g, device=dev).to(dt)
+        vp = torch.randn(n_pages, page, kvs, generator=g, device=dev).to(dt)
+        perm = rng.permutation(n_pages)
+        t = np.full((B, stride), -1, np.int32)
+        i = 0
+        for b in range(B):
+            t[b, :need[b]] = perm[i:i + need[b]]
+            i += need[b]
+        pools.append((kp, vp))
+        tables.append(torch.from_numpy(t).to(dev))
+    q = torch.randn(n_layer, B, H, D, generator=g, device=dev)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = torch.empty(n_layer, B, H, D, device=dev)
+    nws = int(A.L.lib().ullm_hip_paged_decode_workspace_bytes(B, H, Hk, D, L_, 0))
+    ws = torch.zeros(max(nws, 256), dtype=torch.uint8, device=dev)
+
+    def paged_step():
+        for li in range(n_layer):
+            kp, vp = pools[li % n_pool]
+            A.attn_decode_paged(q[li], kp, vp, tables[li % n_pool], sl, L_, Hk, out=out[li],
+                                workspace=ws)
+
+    cont = []
+    for _ in range(n_pool):
+        kc = torch.randn(B, L_, kvs, generator=g, device=dev).to(dt)
+        vc = torch.randn(B, L_, kvs, generator=g, device=dev).to(dt)
+        cont.append((kc, vc))
+    wsc = A.new_decode_workspace(B, H, Hk, D, L_)
+
+    def cont_step():
+        for li in range(n_layer):
+            kc, vc = cont[li % n_pool]
+            A.attn_decode(q[li], kc, vc, sl, L_, Hk, out=out[li], seq_stride=L_ * kvs,
+                          workspace=wsc)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            with torch.cuda.graph(gr, stream=st):
+                fn()
+        torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        for _ in range(2):
+            gr.replay()
+        torch.cuda.synchronize()
+        n = max(3, min(args.steps // 30, 10))
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(n):
+            gr.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) * 1e3 / (n * n_layer)
+
+    us_p = timed(paged_step)
+    us_c = timed(cont_step)
+    lb = sum(lens) * 2 * Hk * D * torch.finfo(dt).bits // 8
+    return dict(lens=lens, page=page, us_paged=us_p, us_contig=us_c, layer_bytes=lb,
+                gbps_paged=lb / (us_p * 1e3), gbps_contig=lb / (us_c * 1e3))
+
+
 def bench_copy(torch):
     """Plain copy of known size: the calibration kernel for FETCH/WRITE_SIZE."""
     n = 256 << 20
@@ -356,6 +443,9 @@ def main():
         res["proj"] = bench_proj(torch, A, args, 2560, 32, 8, 128, torch.bfloat16)
     if args.only in ("all", "matmul"):
         res["matmul"] = bench_matmul(torch, A, args, 2048, 2560, (4096, 1024, 1024))
+    if args.only in ("all", "paged"):
+        res["paged"] = bench_paged(torch, A, args, 32, 4, 128, 8, 4096, 32768, 48, 256,
+                                   torch.bfloat16)
     if args.only in ("all", "long"):
         res["cfg5"] = bench_decode(torch, A, argparse.Namespace(steps=max(5, args.steps // 10),
                                                                 warmup=3),
@@ -365,7 +455,7 @@ def main():
         return
 
     d, p, lc, ap, pj = res["cfg2"], res["cfg3"], res["cfg5"], res["append"], res["proj"]
-    mm = res["matmul"]
+    mm, pg = res["matmul"], res["paged"]
     traffic = load_traffic()
     line = {
         "metric": METRIC,
@@ -420,6 +510,17 @@ def main():
                          "frac_mfma": round(mm["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
                          "note": "activations run as bf16 hi + lo: the matrix cores "
                                  "execute 2x the algorithmic FLOP"},
+        "paged_decode": {"workload": "cfg5 batch 8, ragged lengths in [4096, 32768] "
+                                     f"(SplitMix64: {pg['lens']}), 32/4 heads, head_dim 128, "
+                                     "bf16, 48 layers; paged cache with "
+                                     f"{pg['page']}-position pages shuffled over the pool, and "
+                                     "the contiguous layout for comparison",
+                         "us_per_layer": round(pg["us_paged"], 3),
+                         "gbps": round(pg["gbps_paged"], 1),
+                         "frac_hbm": round(pg["gbps_paged"] / HBM_PEAK_GBS, 4),
+                         "contiguous_us_per_layer": round(pg["us_contig"], 3),
+                         "contiguous_gbps": round(pg["gbps_contig"], 1),
+                         "algorithmic_bytes": pg["layer_bytes"]},
         "roofline": {"bound": "hbm", "achieved": round(d["gbps_step"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["gbps_step"] / HBM_PEAK_GBS, 4),

@@ -175,6 +175,37 @@ size_t ullm_hip_qkv_proj_workspace_bytes(int rows, int n_head, int n_kv_head, in
 int ullm_hip_matmul(const void *w, int w_dtype, const float *x, float *y, int in_dim,
                     int out_dim, int n_cols, void *stream);
 
+/* Bytes of workspace ullm_hip_attn_decode_paged needs (same meaning and
+ * zero-once rule as ullm_hip_decode_workspace_bytes). */
+size_t ullm_hip_paged_decode_workspace_bytes(int batch, int n_head, int n_kv_head, int head_dim,
+                                             int max_len, int window);
+
+/* Decode attention over a PAGED KV cache: the same result as
+ * ullm_hip_attn_decode for batch > 1 with sequences of different lengths
+ * whose positions live in fixed-size pages of a shared pool.  No
+ * counterpart in the reference (its cache is one contiguous [n_ctx][kv_dim]
+ * array per layer, crates/ullm-model/src/lib.rs:184-185, capped at 8192
+ * positions, lib.rs:236); it is the paged/batched cache the reference's
+ * roadmap names (docs/roadmap.md, Phase 2).
+ * k_pages,
+ * v_pages:     pools of n_pages pages; page p holds page_size positions of
+ *              kv_stride elements: element (slot i, kv head j, d) at
+ *              (p*page_size + i)*kv_stride + j*head_dim + d
+ * block_table: DEVICE int32[batch][table_stride]; position t of sequence b
+ *              is slot t % page_size of page block_table[b][t / page_size].
+ *              Entries for pages holding positions in the attended range
+ *              must lie in [0, n_pages) (others are read as zeros)
+ * page_size:   a power of two >= 32; table_stride >= ceil(max_len/page_size)
+ * Other arguments as for ullm_hip_attn_decode.  Slots past a sequence's
+ * length may hold anything (they are masked and their V rows zeroed).
+ * kv_dtype f16 or bf16, head_dim 64 or 128 (else ULLM_HIP_E_UNSUPPORTED). */
+int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, const void *v_pages,
+                               int kv_dtype, int64_t kv_stride, int page_size, int n_pages,
+                               const int32_t *block_table, int table_stride,
+                               const int32_t *seq_lens, int max_len, int window, int batch,
+                               int n_head, int n_kv_head, int head_dim, float scale, float *out,
+                               void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -137,3 +137,24 @@ def test_matmul_validation():
     assert call(i=1 << 20, o=1 << 11) == L.E_INVALID  # 4 GiB weight
     assert call(n=0) == L.OK  # nothing to do
     assert call() == L.E_INVALID  # null pointers
+
+
+def test_paged_decode_validation():
+    f = L.lib().ullm_hip_attn_decode_paged
+
+    def call(**kw):
+        a = dict(q=None, kp=None, vp=None, dt=L.DT_BF16, kvs=512, page=64, npages=10, tab=None,
+                 ts=64, sl=None, ml=4096, win=0, b=1, h=16, hk=4, d=128, sc=0.1, out=None,
+                 ws=None, wsb=0, st=None)
+        a.update(kw)
+        return f(*a.values())
+
+    assert call(dt=L.DT_F32) == L.E_UNSUPPORTED
+    assert call(d=256) == L.E_UNSUPPORTED
+    assert call(page=48) == L.E_INVALID  # not a power of two
+    assert call(page=16) == L.E_INVALID  # below one 32-key block
+    assert call(ts=63) == L.E_INVALID   # table too short for max_len
+    assert call(hk=3) == L.E_INVALID
+    assert call(kvs=500) == L.E_INVALID
+    assert call(npages=0) == L.E_INVALID
+    assert call() == L.E_INVALID  # null pointers

@@ -82,6 +82,42 @@ def attn_decode(q, k_cache, v_cache, seq_lens, max_len, n_kv_head, *, window=0, 
     return out
 
 
+def attn_decode_paged(q, k_pages, v_pages, block_table, seq_lens, max_len, n_kv_head, *,
+                      window=0, scale=None, out=None, workspace=None, stream=None):
+    """Decode attention over a paged KV cache (same result as attn_decode).
+
+    q: [B, n_head, D] f32.  k_pages/v_pages: [n_pages, page_size, kv_stride]
+    f16/bf16.  block_table: int32 [B, table_stride] (page of position t of
+    sequence b = block_table[b, t // page_size]).  seq_lens: int32 [B].
+    """
+    B, H, D = q.shape
+    _need_cuda(q, k_pages, v_pages, block_table, seq_lens)
+    if q.dtype != torch.float32 or not q.is_contiguous():
+        raise L.UllmHipError(L.E_INVALID, "q must be contiguous f32 [B, n_head, head_dim]")
+    if k_pages.dim() != 3 or k_pages.shape != v_pages.shape or not k_pages.is_contiguous() \
+            or not v_pages.is_contiguous():
+        raise L.UllmHipError(L.E_INVALID, "k_pages/v_pages must be contiguous [n_pages, page_size, kv_stride]")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B \
+            or not block_table.is_contiguous():
+        raise L.UllmHipError(L.E_INVALID, "block_table must be contiguous int32 [B, table_stride]")
+    if seq_lens.dtype != torch.int32 or seq_lens.numel() != B:
+        raise L.UllmHipError(L.E_INVALID, "seq_lens must be int32 [B]")
+    n_pages, page_size, kv_stride = k_pages.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty(B, H, D, dtype=torch.float32, device=q.device)
+    if workspace is None:
+        n = int(L.lib().ullm_hip_paged_decode_workspace_bytes(B, H, n_kv_head, D, max_len, window))
+        workspace = torch.zeros(max(n, 256), dtype=torch.uint8, device=q.device)
+    rc = L.lib().ullm_hip_attn_decode_paged(
+        _ptr(q), _ptr(k_pages), _ptr(v_pages), _dt(k_pages), kv_stride, page_size, n_pages,
+        _ptr(block_table), block_table.shape[1], _ptr(seq_lens), max_len, window, B, H, n_kv_head,
+        D, float(scale), _ptr(out), _ptr(workspace), workspace.numel(), _stream(stream))
+    L.check(rc)
+    return out
+
+
 def attn_prefill(q, k_cache, v_cache, n_head, n_kv_head, head_dim, *, start_pos=0, window=0,
                  scale=None, kv_stride=None, out=None, stream=None):
     """Causal prefill attention on MFMA (lib.rs:1061-1087).

@@ -340,13 +340,25 @@ namespace ullm {
 // ds_read_b128, V^T operands from the transposing ds_read_b64_tr_b16.  Each
 // wave owns two stages (double buffering); the wait for a stage leaves the
 // other stage's transfers in flight.
+//
+// PG (paged cache): kc/vc are pools of pages of 2^page_shift token rows
+// (kv_stride elements each); token t of sequence b lives in row t % P of
+// page ptab[b * ptab_stride + t / P].  Every 32-key block lies inside one
+// page (P is a multiple of 32), so a block's DMA goes through a buffer
+// resource based at its page, whose range (one page; zero for a page index
+// outside [0, n_pages)) bounds every read.  With a binding window the blocks
+// start at the window start rounded down to 32 keys and the keys before it
+// are masked.  Rows outside [start, length) hold whatever the page holds
+// there: their V rows are zeroed in LDS (P is 0 for them, but 0 * NaN is
+// NaN).
 
-template <class T, int D, int MW>
+template <class T, int D, int MW, bool PG = false>
 __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
     int fetch_len, int n_head, int kv_mul, int gt, int n_units, int chunk, int splits, float qscale,
-    float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc) {
+    float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc,
+    const int32_t *__restrict__ ptab, int ptab_stride, int page_shift, int n_pages) {
     constexpr int NS = D / 32;          // QK k-steps (32 d each)
     constexpr int NDT = D / 16;         // 16-wide d tiles of O^T
     constexpr int RB = D * 2;           // bytes per key row of one head
@@ -391,7 +403,7 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
     };
     if (fetch_len <= 0) take_len();
     const int start = (fetch_len > 0 || window <= 0 || len <= window) ? 0 : len - window;
-    const int c0 = (fetch_len > 0 ? 0 : start) + split * chunk;
+    const int c0 = (fetch_len > 0 ? 0 : (PG ? start & ~(kTok - 1) : start)) + split * chunk;
     const int cf = fetch_len > 0 ? min(c0 + chunk, fetch_len) : min(c0 + chunk, len);
 
     const int rb = (int)(kv_stride * 2);
@@ -412,14 +424,33 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
         dofs[i] = r * rb + ((dslot ^ (r & (SLOTS - 1))) * 16);
     }
     auto issue = [&](char *kt, int tb) {
-        const int so = __builtin_amdgcn_readfirstlane(tb * rb);
         char *vt = kt + TILE;
+        if constexpr (PG) {
+            const int pg = __builtin_amdgcn_readfirstlane(tb >> page_shift);
+            const int phys = ptab[(int64_t)b * ptab_stride + pg];
+            const bool ok = phys >= 0 && phys < n_pages;
+            const int64_t pb = ((int64_t)(ok ? phys : 0) << page_shift) * rb + (int64_t)kvh * D * 2;
+            const int prange = ok ? (rb << page_shift) : 0;
+            const __amdgpu_buffer_rsrc_t kp =
+                __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + pb), 0, prange, kRsrcWord3);
+            const __amdgpu_buffer_rsrc_t vp =
+                __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + pb), 0, prange, kRsrcWord3);
+            const int so = __builtin_amdgcn_readfirstlane((tb & ((1 << page_shift) - 1)) * rb);
 #pragma unroll
-        for (int i = 0; i < NI; i++)
-            dma16(krs, kt + i * 1024, dofs[i] + so, 0);
+            for (int i = 0; i < NI; i++)
+                dma16(kp, kt + i * 1024, dofs[i] + so, 0);
 #pragma unroll
-        for (int i = 0; i < NI; i++)
-            dma16(vrs, vt + i * 1024, dofs[i] + so, 0);
+            for (int i = 0; i < NI; i++)
+                dma16(vp, vt + i * 1024, dofs[i] + so, 0);
+        } else {
+            const int so = __builtin_amdgcn_readfirstlane(tb * rb);
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+                dma16(krs, kt + i * 1024, dofs[i] + so, 0);
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+                dma16(vrs, vt + i * 1024, dofs[i] + so, 0);
+        }
     };
 
     // q goes out first: waiting for it then leaves the K/V stages in flight.
@@ -494,6 +525,13 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
                 for (int i = 0; i < 4; i++)
                     if (tb + t * 16 + kg * 4 + i >= c1) sv[t * 4 + i] = -INFINITY;
         }
+        if (PG && tb < start) {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (tb + t * 16 + kg * 4 + i < start) sv[t * 4 + i] = -INFINITY;
+        }
         float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                          fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
         mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
@@ -521,12 +559,18 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
                 ph[j] = pack2<T>(p[2 * j], p[2 * j + 1]);
             }
         }
-        if (fetch_len > 0 && tb + kTok > c1) {
+        if ((fetch_len > 0 || PG) && tb + kTok > c1) {
             // Fetched rows at or past the length hold whatever the cache
             // holds there (P is 0 for them, but 0 * NaN is NaN): zero them.
             const uint32_t vz = lds_addr(vt);
             const int nv = max(c1 - tb, 0);
             for (int i = nv * SLOTS + lane; i < kTok * SLOTS; i += 64)
+                lds_write_b128(vz + i * 16, u32x4{0u, 0u, 0u, 0u});
+        }
+        if (PG && tb < start) {  // rows of the first block before the window start
+            const uint32_t vz = lds_addr(vt);
+            const int nz = min(start - tb, kTok);
+            for (int i = lane; i < nz * SLOTS; i += 64)
                 lds_write_b128(vz + i * 16, u32x4{0u, 0u, 0u, 0u});
         }
         // O^T += V^T . P^T; lane n16 of key group kg reads V rows kg*4 + n16/4
@@ -750,9 +794,10 @@ template <class T, int D, bool DMA = (D <= 128)>
 struct MainLaunch {
     template <class... A>
     static void run(int mw, dim3 g, hipStream_t st, A... a) {
-        if (mw == 1) hipLaunchKernelGGL((decode_dma_kernel<T, D, 1>), g, dim3(64), 0, st, a...);
-        else if (mw == 2) hipLaunchKernelGGL((decode_dma_kernel<T, D, 2>), g, dim3(128), 0, st, a...);
-        else hipLaunchKernelGGL((decode_dma_kernel<T, D, kMW>), g, dim3(kMW * 64), 0, st, a...);
+        const int32_t *nt = nullptr;
+        if (mw == 1) hipLaunchKernelGGL((decode_dma_kernel<T, D, 1>), g, dim3(64), 0, st, a..., nt, 0, 0, 0);
+        else if (mw == 2) hipLaunchKernelGGL((decode_dma_kernel<T, D, 2>), g, dim3(128), 0, st, a..., nt, 0, 0, 0);
+        else hipLaunchKernelGGL((decode_dma_kernel<T, D, kMW>), g, dim3(kMW * 64), 0, st, a..., nt, 0, 0, 0);
     }
 };
 template <class T, int D>
@@ -762,6 +807,22 @@ struct MainLaunch<T, D, false> {
         hipLaunchKernelGGL((decode_mfma_kernel<T, D>), g, dim3(kMW * 64), 0, st, a...);
     }
 };
+
+template <int D>
+static void launch_merge(const MfmaPlan &p, int batch, int nh, float *out, char *ws, hipStream_t st) {
+    constexpr int R = kMergeThreads / (D / 4 / kMergeGroups);
+    const int nl = (p.splits + R - 1) / R;
+    const dim3 g(p.gt * kMergeGroups, p.n_units, batch);
+    const float *ml = (const float *)(ws + p.off_ml), *ac = (const float *)(ws + p.off_acc);
+#define ULLM_MERGE(NL) hipLaunchKernelGGL((decode_merge_kernel<D, NL>), g, dim3(kMergeThreads), 0, \
+                                          st, ml, ac, p.splits, p.gt, p.n_units, nh, out)
+    if (nl <= 1) ULLM_MERGE(1);
+    else if (nl <= 2) ULLM_MERGE(2);
+    else if (nl <= 4) ULLM_MERGE(4);
+    else if (nl <= 8) ULLM_MERGE(8);
+    else ULLM_MERGE(16);
+#undef ULLM_MERGE
+}
 
 template <class T, int D>
 static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const void *vc,
@@ -776,20 +837,7 @@ static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const
                           p.n_units,
                           p.chunk, p.splits, qs, out, (float *)(ws + p.off_ml),
                           (float *)(ws + p.off_acc));
-    if (p.splits > 1) {
-        constexpr int R = kMergeThreads / (D / 4 / kMergeGroups);
-        const int nl = (p.splits + R - 1) / R;
-        const dim3 g(p.gt * kMergeGroups, p.n_units, batch);
-        const float *ml = (const float *)(ws + p.off_ml), *ac = (const float *)(ws + p.off_acc);
-#define ULLM_MERGE(NL) hipLaunchKernelGGL((decode_merge_kernel<D, NL>), g, dim3(kMergeThreads), 0, \
-                                          st, ml, ac, p.splits, p.gt, p.n_units, nh, out)
-        if (nl <= 1) ULLM_MERGE(1);
-        else if (nl <= 2) ULLM_MERGE(2);
-        else if (nl <= 4) ULLM_MERGE(4);
-        else if (nl <= 8) ULLM_MERGE(8);
-        else ULLM_MERGE(16);
-#undef ULLM_MERGE
-    }
+    if (p.splits > 1) launch_merge<D>(p, batch, nh, out, ws, st);
 }
 
 int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64_t kvs,
@@ -819,3 +867,101 @@ int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64
 }
 
 }  // namespace ullm
+
+// ---------------------------------------------------------------------------
+// Paged KV cache (no counterpart in the reference, whose cache is one
+// contiguous [n_ctx][kv_dim] array per layer, crates/ullm-model/src/lib.rs:
+// 184-185; the reference's roadmap lists a paged cache for batching,
+// docs/roadmap.md Phase 2).  Same split-KV kernels over a block table.
+namespace ullm {
+
+// Window used for planning: blocks start at the window start rounded down to
+// 32 keys, so a binding window covers up to window + 31 keys.
+static int paged_plan_window(int window) { return window > 0 ? window + kTok : 0; }
+
+template <class T, int D>
+static void launch_paged(const MfmaPlan &p, const float *q, const void *kp, const void *vp,
+                         int64_t kvs, const int32_t *tab, int tab_stride, int shift, int n_pages,
+                         const int32_t *lens, int win, int batch, int nh, int kv_mul, float qs,
+                         float *out, char *ws, hipStream_t st) {
+    const dim3 g(p.splits, p.n_units, batch);
+    auto go = [&](auto mwc) {
+        constexpr int MW = decltype(mwc)::value;
+        hipLaunchKernelGGL((decode_dma_kernel<T, D, MW, true>), g, dim3(MW * 64), 0, st, q,
+                           (const char *)kp, (const char *)vp, kvs, (int64_t)0, lens, win, 0, nh,
+                           kv_mul, p.gt, p.n_units, p.chunk, p.splits, qs, out,
+                           (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), tab, tab_stride,
+                           shift, n_pages);
+    };
+    if (p.mw == 1) go(Int<1>{});
+    else if (p.mw == 2) go(Int<2>{});
+    else go(Int<kMW>{});
+    if (p.splits > 1) launch_merge<D>(p, batch, nh, out, ws, st);
+}
+
+}  // namespace ullm
+
+using namespace ullm;
+
+extern "C" size_t ullm_hip_paged_decode_workspace_bytes(int batch, int n_head, int n_kv_head,
+                                                        int head_dim, int max_len, int window) {
+    if (batch < 1 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || max_len < 1) return 0;
+    if (head_dim != 64 && head_dim != 128) return 0;
+    return decode_mfma_workspace(batch, n_head, n_kv_head, head_dim, max_len,
+                                 paged_plan_window(window));
+}
+
+extern "C" int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, const void *v_pages,
+                                          int kv_dtype, int64_t kv_stride, int page_size,
+                                          int n_pages, const int32_t *block_table,
+                                          int table_stride, const int32_t *seq_lens, int max_len,
+                                          int window, int batch, int n_head, int n_kv_head,
+                                          int head_dim, float scale, float *out, void *workspace,
+                                          size_t workspace_bytes, void *stream) {
+    if (kv_dtype != ULLM_DT_F16 && kv_dtype != ULLM_DT_BF16)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "decode_paged: kv dtype %d (f16/bf16 only)", kv_dtype);
+    if (head_dim != 64 && head_dim != 128)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "decode_paged: head_dim %d not in {64,128}", head_dim);
+    if (batch < 1 || batch > 65535 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head)
+        return set_error(ULLM_HIP_E_INVALID, "decode_paged: bad heads n_head=%d n_kv_head=%d batch=%d",
+                         n_head, n_kv_head, batch);
+    if (max_len < 1) return set_error(ULLM_HIP_E_INVALID, "decode_paged: max_len %d < 1", max_len);
+    if (kv_stride < (int64_t)n_kv_head * head_dim || (kv_stride * 2) % 16)
+        return set_error(ULLM_HIP_E_INVALID,
+                         "decode_paged: kv_stride %lld must be >= n_kv_head*head_dim and 16-byte aligned",
+                         (long long)kv_stride);
+    if (page_size < kTok || (page_size & (page_size - 1)))
+        return set_error(ULLM_HIP_E_INVALID, "decode_paged: page_size %d must be a power of two >= %d",
+                         page_size, kTok);
+    if ((int64_t)page_size * kv_stride * 2 > 0x7fff0000LL)
+        return set_error(ULLM_HIP_E_INVALID, "decode_paged: a page exceeds 2 GiB");
+    if (n_pages < 1) return set_error(ULLM_HIP_E_INVALID, "decode_paged: n_pages %d < 1", n_pages);
+    if (table_stride < (max_len + page_size - 1) / page_size)
+        return set_error(ULLM_HIP_E_INVALID, "decode_paged: table_stride %d < %d pages of max_len",
+                         table_stride, (max_len + page_size - 1) / page_size);
+    if (!q || !k_pages || !v_pages || !block_table || !seq_lens || !out)
+        return set_error(ULLM_HIP_E_INVALID, "decode_paged: null tensor pointer");
+    if (((uintptr_t)k_pages | (uintptr_t)v_pages | (uintptr_t)q) & 15)
+        return set_error(ULLM_HIP_E_INVALID, "decode_paged: q/k_pages/v_pages must be 16-byte aligned");
+    const MfmaPlan p = plan_mfma(batch, n_head, n_kv_head, head_dim, max_len, paged_plan_window(window));
+    if (p.bytes > 0 && (!workspace || workspace_bytes < p.bytes))
+        return set_error(ULLM_HIP_E_WORKSPACE, "decode_paged: workspace of %zu bytes needed, %zu given",
+                         p.bytes, workspace_bytes);
+    const int shift = __builtin_ctz(page_size);
+    const float qs = scale * kLog2e;
+    const int kv_mul = n_head / n_kv_head;
+    char *w = (char *)workspace;
+    hipStream_t st = (hipStream_t)stream;
+#define ULLM_PAGED(TT, DD) \
+    launch_paged<TT, DD>(p, q, k_pages, v_pages, kv_stride, block_table, table_stride, shift, n_pages, \
+                         seq_lens, window, batch, n_head, kv_mul, qs, out, w, st)
+    if (kv_dtype == ULLM_DT_F16) {
+        if (head_dim == 64) ULLM_PAGED(F16, 64);
+        else ULLM_PAGED(F16, 128);
+    } else {
+        if (head_dim == 64) ULLM_PAGED(BF16, 64);
+        else ULLM_PAGED(BF16, 128);
+    }
+#undef ULLM_PAGED
+    return check_hip(hipGetLastError(), "decode_paged launch");
+}
