@@ -254,11 +254,12 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
                     sacc[kt][i] = dead ? -INFINITY : sacc[kt][i];
                 }
         }
-        float mloc = -INFINITY;
+        float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // independent chains
 #pragma unroll
         for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) mloc = fmaxf(mloc, sacc[kt][i]);
+            for (int i = 0; i < 16; i++) m4[i & 3] = fmaxf(m4[i & 3], sacc[kt][i]);
+        float mloc = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * qscale;
         const float m_new = fmaxf(m_run, mloc);
         const float mu = m_new == -INFINITY ? 0.f : m_new;
@@ -270,6 +271,7 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
         }
         m_run = m_new;
         u32x4 ph[NKT][2];
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};  // independent partial sums
 #pragma unroll
         for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
@@ -278,9 +280,10 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
                 for (int jj = 0; jj < 4; jj++) {
                     const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][ks * 8 + 2 * jj], qscale, -mu));
                     const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][ks * 8 + 2 * jj + 1], qscale, -mu));
-                    l_part += p0 + p1;
+                    ls[jj] += p0 + p1;
                     ph[kt][ks][jj] = pack_f16x2(p0, p1);
                 }
+        l_part += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 
         // ---- O^T += V^T . P^T: two transposing reads per 16-key k-step ----
         const int g16 = lane >> 4, i16 = lane & 15, hh = g16 >> 1;
@@ -571,12 +574,12 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     // Row max of s2[SRC], in the exp2 domain.
     auto rowmax = [&](auto srcc) {
         constexpr int SRC = decltype(srcc)::value;
-        float mloc = -INFINITY;
+        float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // independent chains
 #pragma unroll
         for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) mloc = fmaxf(mloc, s2[SRC][kt][i]);
-        return max_xor32(mloc) * qscale;
+            for (int i = 0; i < 16; i++) m4[i & 3] = fmaxf(m4[i & 3], s2[SRC][kt][i]);
+        return max_xor32(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]))) * qscale;
     };
     // Lazy online-softmax max update before an item's exponentials.
     auto raise_max = [&](float mloc) {
@@ -593,6 +596,9 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     auto exps = [&](auto srcc) {
         constexpr int SRC = decltype(srcc)::value;
         const float mu = m_run == -INFINITY ? 0.f : m_run;
+        // Four independent partial sums: one running sum would chain every
+        // add of the step behind the previous one.
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
@@ -602,8 +608,9 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
                     const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s2[SRC][kt][ks * 8 + 2 * jj], qscale, -mu));
                     const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s2[SRC][kt][ks * 8 + 2 * jj + 1], qscale, -mu));
                     ph[kt][ks][jj] = pack_f16x2(p0, p1);
-                    l_part += p0 + p1;
+                    ls[jj] += p0 + p1;
                 }
+        l_part += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     };
     // O += V^T P with the item's V in V stage 2 VPAR + set.  The V^T reads of
     // d tile dt + 1 are in flight during dt's MFMAs.
@@ -961,15 +968,17 @@ __global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
         }
         const float mu = m_run == -INFINITY ? 0.f : m_run;
         u32x4 pk[2];
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};  // independent partial sums
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) {
                 const float p0 = __builtin_amdgcn_exp2f(sacc[ks * 8 + 2 * jj] - mu);
                 const float p1 = __builtin_amdgcn_exp2f(sacc[ks * 8 + 2 * jj + 1] - mu);
-                l_part += p0 + p1;
+                ls[jj] += p0 + p1;
                 pk[ks][jj] = pack_f16x2(p0, p1);
             }
+        l_part += (ls[0] + ls[1]) + (ls[2] + ls[3]);
         // O^T += V^T . P^T, the V^T reads of d tile dt + 1 in flight during dt's MFMAs
         u32x2 vb[2][2][2];
         auto rd = [&](int dt, int buf) {
