@@ -127,15 +127,29 @@ def bench_prefill(torch, A, args, S, H, Hk, D, dt):
     for _ in range(max(3, args.warmup)):
         run()
     torch.cuda.synchronize()
-    n = max(10, min(args.steps, 100))
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(n)]
-    for a, b in ev:
-        a.record()
-        run()
-        b.record()
+    # A graph of back-to-back launches: the events bracket GPU work only, not
+    # per-launch event and dispatch gaps.
+    reps = 20
+    gr = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(gr, stream=st):
+            for _ in range(reps):
+                run()
+    torch.cuda.current_stream().wait_stream(st)
     torch.cuda.synchronize()
-    ms = sum(a.elapsed_time(b) for a, b in ev) / n
+    gr.replay()
+    torch.cuda.synchronize()
+    n = max(3, min(args.steps // 20, 20))
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(n):
+        gr.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / (n * reps)
+    n = n * reps
     flop = 4.0 * D * H * S * (S + 1) / 2  # causal pairs only
     return dict(ms=ms, tflops=flop / (ms * 1e-3) / 1e12, flop=flop, launches=n)
 

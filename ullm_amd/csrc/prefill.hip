@@ -681,9 +681,14 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
         set_barrier();  // item j's V and item j+1's K ready; item j's K and j-1's V consumed
         load_tile(0, j + 2);
         {
+            // The exp + QK phase runs at raised wave priority: the SIMD's
+            // other wave (the other set, often in its PV phase) then fills
+            // the gaps this phase's dependent VALU leaves (3-4 % on cfg3).
+            __builtin_amdgcn_s_setprio(3);
             exps(par);
             qk(npar, npar);  // item j+1 (an idle tile of zeros past the end)
             if (set == 0 && gB >= 0 && j + 1 == TA - 1) load_q(rowB);
+            __builtin_amdgcn_s_setprio(0);
         }
         load_tile(1, j + 1);
         {
