@@ -427,7 +427,9 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
         char *vt = kt + TILE;
         if constexpr (PG) {
             const int pg = __builtin_amdgcn_readfirstlane(tb >> page_shift);
-            const int phys = ptab[(int64_t)b * ptab_stride + pg];
+            // A table index past the row (a length above max_len) is an
+            // invalid page too: never read past the caller's table.
+            const int phys = pg < ptab_stride ? ptab[(int64_t)b * ptab_stride + pg] : -1;
             const bool ok = phys >= 0 && phys < n_pages;
             const int64_t pb = ((int64_t)(ok ? phys : 0) << page_shift) * rb + (int64_t)kvh * D * 2;
             const int prange = ok ? (rb << page_shift) : 0;
