@@ -362,3 +362,65 @@ class GpuAttention:
         return attn_prefill(qr, self.key_cache[layer], self.val_cache[layer], p.n_head,
                             p.n_kv_head, p.head_dim, start_pos=start_pos,
                             window=self._window(layer), scale=self.scale)
+
+    # ---- attention blocks from the normed hidden state ----
+
+    def forward_proj(self, layer: int, xb, pos: int, wq, wk, wv, q_norm=None, k_norm=None,
+                     q_bias=None, k_bias=None, v_bias=None):
+        """Decode one token from the attention-normed hidden state xb [n_embd]
+        f32 (forward.rs:415-466): the Q/K/V matvecs with bias, norm, RoPE and
+        the cache store fused into one launch, then decode attention."""
+        p = self.p
+        if not 0 <= pos < p.n_ctx:
+            raise L.UllmHipError(L.E_INVALID, f"pos {pos} outside the context")
+        qr = qkv_proj_append(xb.view(1, -1), wq, wk, wv, self.key_cache[layer],
+                             self.val_cache[layer], self.rope_cs, start_pos=pos,
+                             n_head=p.n_head, n_kv_head=p.n_kv_head, head_dim=p.head_dim,
+                             rotary_dim=self.rotary_dim, neox=p.rope_neox, q_norm=q_norm,
+                             k_norm=k_norm, eps=p.eps, q_bias=q_bias, k_bias=k_bias,
+                             v_bias=v_bias, q_dtype=torch.float32)
+        self._len.fill_(pos + 1)
+        out = attn_decode(qr.view(1, p.n_head, p.head_dim), self.key_cache[layer],
+                          self.val_cache[layer], self._len, pos + 1, p.n_kv_head,
+                          window=self._window(layer), scale=self.scale,
+                          workspace=self.workspace)
+        return out.view(-1)
+
+    def forward_batch_proj(self, layer: int, xbs, wq, wk, wv, start_pos: int = 0, q_norm=None,
+                           k_norm=None, q_bias=None, k_bias=None, v_bias=None):
+        """Prefill S tokens from the attention-normed hidden states xbs
+        [S, n_embd] f32 (forward.rs:799-858): with bf16 weights the three
+        projections run as MFMA matmuls (forward.rs:799-801), then the fused
+        append and causal prefill attention; other weight dtypes use the
+        fused projection kernel over the S rows."""
+        p = self.p
+        S = xbs.shape[0]
+        if start_pos + S > p.n_ctx:
+            raise L.UllmHipError(L.E_INVALID, "prompt exceeds the context")
+        if wq.dtype == torch.bfloat16:
+            q = matmul(wq, xbs)
+            k = matmul(wk, xbs)
+            v = matmul(wv, xbs)
+            return self.forward_batch(layer, q, k, v, start_pos, q_norm, k_norm, q_bias, k_bias,
+                                      v_bias)
+        q_dtype = torch.float32 if p.kv_dtype == torch.float32 else p.kv_dtype
+        qr = qkv_proj_append(xbs, wq, wk, wv, self.key_cache[layer], self.val_cache[layer],
+                             self.rope_cs, start_pos=start_pos, n_head=p.n_head,
+                             n_kv_head=p.n_kv_head, head_dim=p.head_dim,
+                             rotary_dim=self.rotary_dim, neox=p.rope_neox, q_norm=q_norm,
+                             k_norm=k_norm, eps=p.eps, q_bias=q_bias, k_bias=k_bias,
+                             v_bias=v_bias, q_dtype=q_dtype)
+        if p.kv_dtype == torch.float32:
+            lens = torch.arange(start_pos + 1, start_pos + S + 1, dtype=torch.int32,
+                                device=self.device)
+            ws = new_decode_workspace(S, p.n_head, p.n_kv_head, p.head_dim, start_pos + S,
+                                      self._window(layer), self.device)
+            out = attn_decode(qr.view(S, p.n_head, p.head_dim), self.key_cache[layer],
+                              self.val_cache[layer], lens, start_pos + S, p.n_kv_head,
+                              window=self._window(layer), scale=self.scale, seq_stride=0,
+                              workspace=ws)
+            return out.view(S, -1)
+        return attn_prefill(qr, self.key_cache[layer], self.val_cache[layer], p.n_head,
+                            p.n_kv_head, p.head_dim, start_pos=start_pos,
+                            window=self._window(layer), scale=self.scale)
+
