@@ -74,6 +74,8 @@ CASES = [
     ([5000, 3000, 600], 12, 2, 128, "f16", 64, 1024, 0),
     ([5000, 4100, 40], 8, 4, 64, "bf16", 32, 37, 0),
     ([33000, 12000], 32, 4, 128, "bf16", 512, 4096, 0),
+    ([8192, 3000, 1], 8, 4, 256, "f16", 64, 0, 0),       # head_dim 256 (register-staged kernel)
+    ([9000, 2000], 16, 8, 256, "bf16", 256, 1024, 16),
 ]
 
 

@@ -93,12 +93,15 @@ __device__ void finish_unit(const float *sm_m, const float *sm_l, const float *s
     }
 }
 
-template <class T, int D>
+// PG: paged cache, addressed as in decode_dma_kernel below (a block's loads
+// go through a buffer resource based at its page).
+template <class T, int D, bool PG = false>
 __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
     int fetch_len, int n_head, int kv_mul, int gt, int n_units, int chunk, int splits, float qscale,
-    float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc) {
+    float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc,
+    const int32_t *__restrict__ ptab, int ptab_stride, int page_shift, int n_pages) {
     constexpr int NS = D / 32;      // QK k-steps (32 d each)
     constexpr int NDT = D / 16;     // 16-wide d tiles of O^T
     constexpr int CPR = D / 8;      // 16-byte chunks per key row
@@ -129,7 +132,7 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     // (keys past the length are masked (K) and zeroed (V) once it is known).
     const int len = __builtin_amdgcn_readfirstlane(seq_lens[b]);
     const int start = (fetch_len > 0 || window <= 0 || len <= window) ? 0 : len - window;
-    const int c0 = (fetch_len > 0 ? 0 : start) + split * chunk;
+    const int c0 = (fetch_len > 0 ? 0 : (PG ? start & ~(kTok - 1) : start)) + split * chunk;
     const int c1 = min(c0 + chunk, len);
     const int cf = fetch_len > 0 ? min(c0 + chunk, fetch_len) : c1;
 
@@ -172,17 +175,30 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     const int voffb = vrow0 * rb + vcol * 16;
     // Issue the loads of the block starting at key tb (nontemporal).
     auto issue = [&](Tile &T_, int tb) {
-        const int so = __builtin_amdgcn_readfirstlane(tb * rb);
+        __amdgpu_buffer_rsrc_t kr = krs, vr = vrs;
+        int so;
+        if constexpr (PG) {
+            const int pg = __builtin_amdgcn_readfirstlane(tb >> page_shift);
+            const int phys = pg < ptab_stride ? ptab[(int64_t)b * ptab_stride + pg] : -1;
+            const bool ok = phys >= 0 && phys < n_pages;
+            const int64_t pb = ((int64_t)(ok ? phys : 0) << page_shift) * rb + (int64_t)kvh * D * 2;
+            const int prange = ok ? (rb << page_shift) : 0;
+            kr = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + pb), 0, prange, kRsrcWord3);
+            vr = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + pb), 0, prange, kRsrcWord3);
+            so = __builtin_amdgcn_readfirstlane((tb & ((1 << page_shift) - 1)) * rb);
+        } else {
+            so = __builtin_amdgcn_readfirstlane(tb * rb);
+        }
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int s = 0; s < NS; s++)
                 T_.k[t][s] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koffb[t] + s * 64 + so, 0, 2));
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koffb[t] + s * 64 + so, 0, 2));
 #pragma unroll
         for (int i = 0; i < VL; i++)
             T_.v[i] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voffb + i * KPI * rb + so, 0, 2));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voffb + i * KPI * rb + so, 0, 2));
     };
     // Consume a loaded block.
     auto consume = [&](Tile &T_, int tb) {
@@ -202,7 +218,8 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
 #pragma unroll
         for (int i = 0; i < VL; i++) {
             u32x4 vv = T_.v[i];
-            if (fetch_len > 0 && tb + vrow0 + i * KPI >= c1) vv = u32x4{0u, 0u, 0u, 0u};
+            if ((fetch_len > 0 || PG) && tb + vrow0 + i * KPI >= c1) vv = u32x4{0u, 0u, 0u, 0u};
+            if (PG && tb + vrow0 + i * KPI < start) vv = u32x4{0u, 0u, 0u, 0u};
             *(u32x4 *)(vt + (vrow0 + i * KPI) * VP + vcol * 8) = vv;
         }
         // online softmax: lane = head n16, keys kg*4+i (tile 0) and 16+kg*4+i
@@ -217,6 +234,13 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     if (tb + t * 16 + kg * 4 + i >= c1) sv[t * 4 + i] = -INFINITY;
+        }
+        if (PG && tb < start) {  // keys of the first block before the window start
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (tb + t * 16 + kg * 4 + i < start) sv[t * 4 + i] = -INFINITY;
         }
         float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                          fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
@@ -806,7 +830,8 @@ template <class T, int D>
 struct MainLaunch<T, D, false> {
     template <class... A>
     static void run(int, dim3 g, hipStream_t st, A... a) {
-        hipLaunchKernelGGL((decode_mfma_kernel<T, D>), g, dim3(kMW * 64), 0, st, a...);
+        const int32_t *nt = nullptr;
+        hipLaunchKernelGGL((decode_mfma_kernel<T, D>), g, dim3(kMW * 64), 0, st, a..., nt, 0, 0, 0);
     }
 };
 
@@ -887,17 +912,25 @@ static void launch_paged(const MfmaPlan &p, const float *q, const void *kp, cons
                          const int32_t *lens, int win, int batch, int nh, int kv_mul, float qs,
                          float *out, char *ws, hipStream_t st) {
     const dim3 g(p.splits, p.n_units, batch);
-    auto go = [&](auto mwc) {
-        constexpr int MW = decltype(mwc)::value;
-        hipLaunchKernelGGL((decode_dma_kernel<T, D, MW, true>), g, dim3(MW * 64), 0, st, q,
+    if constexpr (D > 128) {  // register-staged kernel, 4 waves
+        hipLaunchKernelGGL((decode_mfma_kernel<T, D, true>), g, dim3(kMW * 64), 0, st, q,
                            (const char *)kp, (const char *)vp, kvs, (int64_t)0, lens, win, 0, nh,
                            kv_mul, p.gt, p.n_units, p.chunk, p.splits, qs, out,
                            (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), tab, tab_stride,
                            shift, n_pages);
-    };
-    if (p.mw == 1) go(Int<1>{});
-    else if (p.mw == 2) go(Int<2>{});
-    else go(Int<kMW>{});
+    } else {
+        auto go = [&](auto mwc) {
+            constexpr int MW = decltype(mwc)::value;
+            hipLaunchKernelGGL((decode_dma_kernel<T, D, MW, true>), g, dim3(MW * 64), 0, st, q,
+                               (const char *)kp, (const char *)vp, kvs, (int64_t)0, lens, win, 0,
+                               nh, kv_mul, p.gt, p.n_units, p.chunk, p.splits, qs, out,
+                               (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), tab,
+                               tab_stride, shift, n_pages);
+        };
+        if (p.mw == 1) go(Int<1>{});
+        else if (p.mw == 2) go(Int<2>{});
+        else go(Int<kMW>{});
+    }
     if (p.splits > 1) launch_merge<D>(p, batch, nh, out, ws, st);
 }
 
@@ -908,7 +941,7 @@ using namespace ullm;
 extern "C" size_t ullm_hip_paged_decode_workspace_bytes(int batch, int n_head, int n_kv_head,
                                                         int head_dim, int max_len, int window) {
     if (batch < 1 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || max_len < 1) return 0;
-    if (head_dim != 64 && head_dim != 128) return 0;
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
     return decode_mfma_workspace(batch, n_head, n_kv_head, head_dim, max_len,
                                  paged_plan_window(window));
 }
@@ -922,8 +955,8 @@ extern "C" int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, c
                                           size_t workspace_bytes, void *stream) {
     if (kv_dtype != ULLM_DT_F16 && kv_dtype != ULLM_DT_BF16)
         return set_error(ULLM_HIP_E_UNSUPPORTED, "decode_paged: kv dtype %d (f16/bf16 only)", kv_dtype);
-    if (head_dim != 64 && head_dim != 128)
-        return set_error(ULLM_HIP_E_UNSUPPORTED, "decode_paged: head_dim %d not in {64,128}", head_dim);
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "decode_paged: head_dim %d not in {64,128,256}", head_dim);
     if (batch < 1 || batch > 65535 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head)
         return set_error(ULLM_HIP_E_INVALID, "decode_paged: bad heads n_head=%d n_kv_head=%d batch=%d",
                          n_head, n_kv_head, batch);
@@ -959,10 +992,12 @@ extern "C" int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, c
                          seq_lens, window, batch, n_head, kv_mul, qs, out, w, st)
     if (kv_dtype == ULLM_DT_F16) {
         if (head_dim == 64) ULLM_PAGED(F16, 64);
-        else ULLM_PAGED(F16, 128);
+        else if (head_dim == 128) ULLM_PAGED(F16, 128);
+        else ULLM_PAGED(F16, 256);
     } else {
         if (head_dim == 64) ULLM_PAGED(BF16, 64);
-        else ULLM_PAGED(BF16, 128);
+        else if (head_dim == 128) ULLM_PAGED(BF16, 128);
+        else ULLM_PAGED(BF16, 256);
     }
 #undef ULLM_PAGED
     return check_hip(hipGetLastError(), "decode_paged launch");
