@@ -95,3 +95,81 @@ def test_prefill_random(dev, seed):
                            v.float().cpu().numpy(), S, sp, H, Hk, D, scale,
                            window=c["window"], rows=rows)
     assert_close(out[rows], ref[rows], what=f"seed={seed} rows {rows[:6]}..")
+
+
+def _matmul_case(seed):
+    rng = np.random.default_rng(3000 + seed)
+    return dict(n=int(rng.integers(1, 1500)), i=8 * int(rng.integers(1, 400)),
+                o=4 * int(rng.integers(1, 800)), xs=float(rng.choice([1.0, 1e-3, 1e3])))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_matmul_random(dev, seed):
+    """Projection GEMM at random shapes (tails in every dimension, both tile
+    variants) against an f64 product of the same rounded inputs, with the
+    bound of tests/test_matmul_gpu.py."""
+    c = _matmul_case(seed)
+    print(f"[matmul-rand] seed={seed} {c}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(c["n"], c["i"], device=dev, generator=g) * c["xs"]
+    w = (torch.randn(c["o"], c["i"], device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    y = A.matmul(w, x)
+    torch.cuda.synchronize()
+    x64, w64 = x.cpu().double().numpy(), w.cpu().double().numpy()
+    ref = x64 @ w64.T
+    bound = (2.0 ** -16 + c["i"] * 2.0 ** -24) * (np.abs(x64) @ np.abs(w64).T) + 1e-30
+    worst = float(np.max(np.abs(y.cpu().double().numpy() - ref) / bound))
+    assert worst <= 1.0, f"seed={seed}: error {worst:.3f} x the bound"
+
+
+def _paged_case(seed):
+    rng = np.random.default_rng(4000 + seed)
+    H, Hk, D = _shape(rng)
+    B = int(rng.integers(1, 6))
+    return dict(H=H, Hk=Hk, D=D, dtype=str(rng.choice(["f16", "bf16"])), B=B,
+                lens=[int(x) for x in rng.integers(1, 9000, size=B)],
+                page=int(rng.choice([32, 64, 128, 256])),
+                window=int(rng.choice([0, 0, 1, 100, 2000])))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_paged_decode_random(dev, seed):
+    """Paged decode at random shapes: pages shuffled over the pool, unused
+    slots NaN, against the oracle on each sequence's gathered rows."""
+    c = _paged_case(seed)
+    print(f"[paged-rand] seed={seed} {c}", flush=True)
+    H, Hk, D, P, lens = c["H"], c["Hk"], c["D"], c["page"], c["lens"]
+    dt = DT[c["dtype"]]
+    B, L_ = len(lens), max(lens)
+    kvs = Hk * D
+    need = [(n + P - 1) // P for n in lens]
+    n_pages = sum(need) + 2
+    perm = np.random.default_rng(seed).permutation(n_pages)
+    kp = torch.full((n_pages, P, kvs), float("nan"), dtype=dt)
+    vp = torch.full_like(kp, float("nan"))
+    stride = (L_ + P - 1) // P
+    table = np.full((B, stride), -1, np.int32)
+    seqs = []
+    i = 0
+    for b, n in enumerate(lens):
+        k = synth.randn(seed, 10 + b, (n, kvs), dt)
+        v = synth.randn(seed, 20 + b, (n, kvs), dt)
+        seqs.append((k, v))
+        for pg in range(need[b]):
+            phys = int(perm[i]); i += 1
+            table[b, pg] = phys
+            r = min(P, n - pg * P)
+            kp[phys, :r] = k[pg * P:pg * P + r]
+            vp[phys, :r] = v[pg * P:pg * P + r]
+    q = synth.randn(seed, 1, (B, H, D)).to(dev)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = A.attn_decode_paged(q, kp.to(dev), vp.to(dev), torch.from_numpy(table).to(dev), sl, L_,
+                              Hk, window=c["window"])
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    qn = q.cpu().numpy()
+    for b, n in enumerate(lens):
+        k, v = seqs[b]
+        ref = ora.attn_decode(qn[b].reshape(-1).copy(), k.float().numpy(), v.float().numpy(), n - 1,
+                              H, Hk, D, 1.0 / math.sqrt(D), window=c["window"])
+        assert_close(o[b].reshape(-1), ref, what=f"seed={seed} b={b}")
