@@ -6,6 +6,7 @@
 #include <stddef.h>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 
 #include "../../include/ullm_hip.h"
 
@@ -86,6 +87,13 @@ __device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p;
 // it from displacing reusable lines.
 __device__ __forceinline__ u32x4 ld16_stream(const void *p) {
     return __builtin_nontemporal_load((const u32x4 *)p);
+}
+
+// Tuning override from the environment (0 when unset), read once when the
+// library loads rather than on every call.
+inline int env_override(const char *name) {
+    const char *e = getenv(name);
+    return e ? atoi(e) : 0;
 }
 
 // Host-side status plumbing -------------------------------------------------

@@ -290,6 +290,8 @@ static int lanes_per_key(int dtype, int D) { return D / (16 / dtype_bytes(dtype)
 // Split-KV plan.  Chunks are multiples of the lane-group count so every lane
 // group gets whole keys; the split count aims at a few workgroups per CU but is
 // capped, because the last workgroup of a unit reads every split's partial.
+static const int kEnvSplits = env_override("ULLM_HIP_DECODE_SPLITS");
+
 static DecodePlan plan_decode(int batch, int n_head, int n_kv_head, int D, int dtype, int max_len,
                               int window) {
     DecodePlan p{};
@@ -309,10 +311,7 @@ static DecodePlan plan_decode(int batch, int n_head, int n_kv_head, int D, int d
     if (splits > want) splits = want;
     const int merge_cap = 256 / p.G;                       // merge reads <= 256 partial rows
     if (splits > merge_cap) splits = merge_cap;
-    if (const char *e = getenv("ULLM_HIP_DECODE_SPLITS")) {  // tuning override
-        const int f = atoi(e);
-        if (f >= 1) splits = f < merge_cap ? f : merge_cap;
-    }
+    if (kEnvSplits >= 1) splits = kEnvSplits < merge_cap ? kEnvSplits : merge_cap;  // tuning override
     if (splits < 1) splits = 1;
     int chunk = (visible + splits - 1) / splits;
     chunk = ((chunk + p.nlg - 1) / p.nlg) * p.nlg;

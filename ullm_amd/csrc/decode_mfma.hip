@@ -754,6 +754,9 @@ struct MfmaPlan {
     size_t off_ml, off_acc, bytes;
 };
 
+static const int kEnvMw = env_override("ULLM_HIP_DECODE_MW");
+static const int kEnvSplitsM = env_override("ULLM_HIP_DECODE_SPLITS");
+
 static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_len, int window) {
     MfmaPlan p{};
     const int kv_mul = n_head / n_kv_head;
@@ -773,8 +776,7 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     const int blocks = (visible + kTok - 1) / kTok;
     if (D > 128 || blocks <= kMW * 4) p.mw = kMW;
     else p.mw = (int64_t)units * blocks <= 1024 ? 1 : 2;
-    if (const char *e = getenv("ULLM_HIP_DECODE_MW"))  // tuning override
-        if (D <= 128 && (atoi(e) == 1 || atoi(e) == 2 || atoi(e) == kMW)) p.mw = atoi(e);
+    if (D <= 128 && (kEnvMw == 1 || kEnvMw == 2 || kEnvMw == kMW)) p.mw = kEnvMw;  // tuning override
     const int tile = p.mw * kTok;
     int splits = (visible + tile - 1) / tile;
     const int want = (kMfmaTargetWG * (p.mw == kMW ? 1 : 2) + units - 1) / units;
@@ -782,10 +784,7 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     if (splits > want) splits = want;
     const int cap = kMaxSplits;
     if (splits > cap) splits = cap;
-    if (const char *e = getenv("ULLM_HIP_DECODE_SPLITS")) {  // tuning override
-        const int f = atoi(e);
-        if (f >= 1) splits = f < cap ? f : cap;
-    }
+    if (kEnvSplitsM >= 1) splits = kEnvSplitsM < cap ? kEnvSplitsM : cap;  // tuning override
     if (splits < 1) splits = 1;
     int chunk = (visible + splits - 1) / splits;
     chunk = (chunk + kTok - 1) / kTok * kTok;
