@@ -436,7 +436,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build targets ONE GPU; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              "(sharding over several GPUs is not built; it runs on one GPU)", file=sys.stderr)
         sys.exit(2)
     import torch
 
