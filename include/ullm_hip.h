@@ -206,6 +206,25 @@ int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, const void *
                                int n_head, int n_kv_head, int head_dim, float scale, float *out,
                                void *workspace, size_t workspace_bytes, void *stream);
 
+/* Batched append into a PAGED cache: row r is the new token of sequence r at
+ * position positions[r] (DEVICE int32[rows]); it gets the same bias, Q/K
+ * norm and RoPE (at its own position) as ullm_hip_qkv_append, q goes to row r
+ * of q_out, and the K/V rows go to slot pos % page_size of page
+ * block_table[r][pos / page_size] (the layout of ullm_hip_attn_decode_paged).
+ * No counterpart in the reference (its cache is contiguous and it decodes
+ * one sequence at a time, crates/ullm-model/src/lib.rs:857-914); it is the
+ * append step of a batched decode over the paged cache.  A row whose
+ * position is outside [0, rope_n_pos) or whose page index is outside the
+ * table or [0, n_pages) writes nothing.  page_size: a power of two. */
+int ullm_hip_qkv_append_paged(const float *q_in, const float *k_in, const float *v_in,
+                              const float *q_bias, const float *k_bias, const float *v_bias,
+                              const float *q_norm, const float *k_norm, float eps,
+                              const float *rope_cs, int rope_n_pos, int rope_neox, int rotary_dim,
+                              int rows, const int32_t *positions, int n_head, int n_kv_head,
+                              int head_dim, void *q_out, int q_dtype, void *k_pages, void *v_pages,
+                              int kv_dtype, int64_t kv_stride, int page_size, int n_pages,
+                              const int32_t *block_table, int table_stride, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -158,3 +158,24 @@ def test_paged_decode_validation():
     assert call(kvs=500) == L.E_INVALID
     assert call(npages=0) == L.E_INVALID
     assert call() == L.E_INVALID  # null pointers
+
+
+def test_paged_append_validation():
+    f = L.lib().ullm_hip_qkv_append_paged
+
+    def call(**kw):
+        a = dict(q=None, k=None, v=None, qb=None, kb=None, vb=None, qn=None, kn=None, eps=1e-6,
+                 cs=None, npos=4096, neox=1, rd=128, rows=4, pos=None, h=16, hk=4, d=128,
+                 qo=None, qdt=L.DT_F32, kp=None, vp=None, kvdt=L.DT_BF16, kvs=512, page=64,
+                 npages=10, tab=None, ts=64, st=None)
+        a.update(kw)
+        return f(*a.values())
+
+    assert call(kvdt=9) == L.E_UNSUPPORTED
+    assert call(d=96) == L.E_UNSUPPORTED
+    assert call(page=48) == L.E_INVALID
+    assert call(hk=3) == L.E_INVALID
+    assert call(kvs=100) == L.E_INVALID
+    assert call(npages=0) == L.E_INVALID
+    assert call(rows=0) == L.OK
+    assert call() == L.E_INVALID  # null pointers

@@ -133,3 +133,107 @@ def test_paged_graph_replay(dev):
         want = A.attn_decode_paged(q, kp, vp, table, sl, L_, Hk)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"replay {it}"
+
+
+@pytest.mark.parametrize("D,kvdt,neox", [(128, "bf16", True), (64, "f16", False), (256, "f16", True)])
+def test_paged_append(dev, D, kvdt, neox):
+    """ullm_hip_qkv_append_paged: each row's K/V land in its own page slot
+    with RoPE at its own position; matches the oracle's append (lib.rs:
+    1021-1058) row by row within one storage ulp; rows with an invalid
+    position or page write nothing."""
+    print(f"[paged-append] D{D} kv={kvdt} neox={neox}", flush=True)
+    H, Hk, page, theta = 8, 2, 64, 1e6
+    pos = [0, 63, 64, 1500, 2999, -1, 700]   # row 5: invalid position
+    rows = len(pos)
+    n_ctx = 3000
+    stride = n_ctx // page + 1
+    rng = np.random.default_rng(D)
+    n_pages = 40
+    table = np.full((rows, stride), -1, np.int32)
+    used = rng.permutation(n_pages)
+    for r, p_ in enumerate(pos):
+        if p_ >= 0:
+            table[r, p_ // page] = used[r]
+    table[6, 700 // page] = n_pages + 3          # row 6: page outside the pool
+    q = synth.randn(D, 1, (rows, H * D))
+    k = synth.randn(D, 2, (rows, Hk * D))
+    v = synth.randn(D, 3, (rows, Hk * D))
+    qn = synth.randn(D, 4, (D,)) * 0.2 + 1.0
+    kn = synth.randn(D, 5, (D,)) * 0.2 + 1.0
+    cs = A.rope_table(n_ctx, D, theta, device=dev)
+    kp = torch.full((n_pages, page, Hk * D), float("nan"), dtype=DT[kvdt], device=dev)
+    vp = torch.full_like(kp, float("nan"))
+    qo = torch.full((rows, H * D), 7.0, device=dev)
+    A.qkv_append_paged(q.to(dev), k.to(dev), v.to(dev), kp, vp, cs,
+                       torch.tensor(pos, dtype=torch.int32, device=dev),
+                       torch.from_numpy(table).to(dev), n_head=H, n_kv_head=Hk, head_dim=D,
+                       neox=neox, q_norm=qn.to(dev), k_norm=kn.to(dev), eps=1e-6, q_out=qo)
+    torch.cuda.synchronize()
+    kp, vp, qo = kp.float().cpu().numpy(), vp.float().cpu().numpy(), qo.cpu().numpy()
+    tol = {"f16": 2e-3, "bf16": 1.6e-2}[kvdt]
+    written = set()
+    for r, p_ in enumerate(pos):
+        if r in (5, 6):
+            assert np.all(qo[r] == 7.0), f"row {r}: skipped row wrote q"
+            continue
+        okc = np.zeros((p_ + 1, Hk * D), np.float32)
+        ovc = np.zeros_like(okc)
+        oq = ora.qkv_append(q[r:r + 1].numpy().copy(), k[r:r + 1].numpy().copy(),
+                            v[r:r + 1].numpy().copy(), p_, H, Hk, D, D, theta, neox, okc, ovc,
+                            q_norm=qn.numpy(), k_norm=kn.numpy(), eps=1e-6)
+        assert np.abs(qo[r] - oq[0]).max() <= 2e-5 * max(1.0, np.abs(oq).max()), f"row {r} q"
+        phys, slot = table[r, p_ // page], p_ % page
+        written.add((phys, slot))
+        for name, got, ref in (("k", kp[phys, slot], okc[p_]), ("v", vp[phys, slot], ovc[p_])):
+            rr = torch.from_numpy(ref).to(DT[kvdt]).float().numpy()
+            rel = np.abs(got - rr) / np.maximum(np.abs(rr), 1.0)
+            assert rel.max() <= tol, f"row {r} {name}: max rel {rel.max():.3e}"
+    # every other slot of the pool is untouched
+    for p_i in range(n_pages):
+        for sl in range(page):
+            if (p_i, sl) not in written:
+                assert np.all(np.isnan(kp[p_i, sl])) and np.all(np.isnan(vp[p_i, sl]))
+
+
+def test_paged_serving_loop(dev):
+    """A batched decode loop over the paged cache: each step appends one
+    token per sequence (paged append) and attends (paged decode); every
+    step's output matches the oracle on the rows the cache then holds."""
+    H, Hk, D, page, n_ctx, theta = 16, 4, 128, 32, 512, 1e6
+    lens = [5, 33, 200]
+    B = len(lens)
+    stride = n_ctx // page
+    n_pages = B * stride
+    perm = np.random.default_rng(3).permutation(n_pages)
+    table = torch.from_numpy(perm.reshape(B, stride).astype(np.int32)).to(dev)
+    kp = torch.full((n_pages, page, Hk * D), float("nan"), dtype=torch.float16, device=dev)
+    vp = torch.full_like(kp, float("nan"))
+    cs = A.rope_table(n_ctx, D, theta, device=dev)
+    kn = (synth.randn(3, 9, (D,)) * 0.2 + 1.0).to(dev)
+    # the prompts: positions 0..len-1 of each sequence, appended row by row
+    for b, n in enumerate(lens):
+        tb = table[b:b + 1].expand(n, stride).contiguous()
+        A.qkv_append_paged(synth.randn(3, 10 + b, (n, H * D)).to(dev),
+                           synth.randn(3, 20 + b, (n, Hk * D)).to(dev),
+                           synth.randn(3, 30 + b, (n, Hk * D)).to(dev), kp, vp, cs,
+                           torch.arange(n, dtype=torch.int32, device=dev), tb, n_head=H,
+                           n_kv_head=Hk, head_dim=D, k_norm=kn)
+    for step in range(4):
+        pos = torch.tensor(lens, dtype=torch.int32, device=dev)
+        qo = A.qkv_append_paged(synth.randn(4, 40 + step, (B, H * D)).to(dev),
+                                synth.randn(4, 50 + step, (B, Hk * D)).to(dev),
+                                synth.randn(4, 60 + step, (B, Hk * D)).to(dev), kp, vp, cs, pos,
+                                table, n_head=H, n_kv_head=Hk, head_dim=D, k_norm=kn)
+        lens = [n + 1 for n in lens]
+        out = A.attn_decode_paged(qo.view(B, H, D), kp, vp, table,
+                                  torch.tensor(lens, dtype=torch.int32, device=dev), n_ctx, Hk)
+        torch.cuda.synchronize()
+        kpc, vpc, tab = kp.float().cpu(), vp.float().cpu(), table.cpu().numpy()
+        for b, n in enumerate(lens):
+            rows = np.array([tab[b, t // page] * page + t % page for t in range(n)])
+            kr = kpc.view(-1, Hk * D)[rows].numpy()
+            vr = vpc.view(-1, Hk * D)[rows].numpy()
+            assert np.all(np.isfinite(kr)) and np.all(np.isfinite(vr)), f"step {step} b={b}"
+            ref = ora.attn_decode(qo[b].cpu().numpy().copy(), kr, vr, n - 1, H, Hk, D,
+                                  1.0 / math.sqrt(D))
+            assert_close(out[b].cpu().numpy().reshape(-1), ref, what=f"step {step} b={b}")

@@ -118,6 +118,42 @@ def attn_decode_paged(q, k_pages, v_pages, block_table, seq_lens, max_len, n_kv_
     return out
 
 
+def qkv_append_paged(q, k, v, k_pages, v_pages, rope_cs, positions, block_table, *, n_head,
+                     n_kv_head, head_dim, rotary_dim=None, neox=True, q_norm=None, k_norm=None,
+                     eps=1e-6, q_bias=None, k_bias=None, v_bias=None, q_out=None, q_dtype=None,
+                     stream=None):
+    """Append one token per sequence into a paged cache: row r of q/k/v [rows,
+    *] f32 is sequence r's token at positions[r] (int32 [rows] on the GPU);
+    its K/V rows land in block_table[r, pos // page_size].  Returns q_out."""
+    rows = q.shape[0]
+    _need_cuda(q, k, v, k_pages, v_pages, rope_cs, positions, block_table)
+    for t in (q, k, v):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise L.UllmHipError(L.E_INVALID, "q/k/v must be contiguous f32")
+    if k_pages.dim() != 3 or k_pages.shape != v_pages.shape:
+        raise L.UllmHipError(L.E_INVALID, "k_pages/v_pages must be [n_pages, page_size, kv_stride]")
+    if positions.dtype != torch.int32 or positions.numel() != rows:
+        raise L.UllmHipError(L.E_INVALID, "positions must be int32 [rows]")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != rows \
+            or not block_table.is_contiguous():
+        raise L.UllmHipError(L.E_INVALID, "block_table must be contiguous int32 [rows, table_stride]")
+    n_pages, page_size, kv_stride = k_pages.shape
+    if rotary_dim is None:
+        rotary_dim = head_dim
+    if q_dtype is None:
+        q_dtype = torch.float32
+    if q_out is None:
+        q_out = torch.empty(rows, n_head * head_dim, dtype=q_dtype, device=q.device)
+    rc = L.lib().ullm_hip_qkv_append_paged(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(q_bias), _ptr(k_bias), _ptr(v_bias), _ptr(q_norm),
+        _ptr(k_norm), float(eps), _ptr(rope_cs), rope_cs.shape[0], int(bool(neox)), rotary_dim,
+        rows, _ptr(positions), n_head, n_kv_head, head_dim, _ptr(q_out), _DT[q_out.dtype],
+        _ptr(k_pages), _ptr(v_pages), _dt(k_pages), kv_stride, page_size, n_pages,
+        _ptr(block_table), block_table.shape[1], _stream(stream))
+    L.check(rc)
+    return q_out
+
+
 def attn_prefill(q, k_cache, v_cache, n_head, n_kv_head, head_dim, *, start_pos=0, window=0,
                  scale=None, kv_stride=None, out=None, stream=None):
     """Causal prefill attention on MFMA (lib.rs:1061-1087).

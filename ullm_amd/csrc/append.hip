@@ -149,18 +149,29 @@ struct HeadEpi {
 };
 
 // Store one finished head vector: q to q_out (row-major [rows][n_head*D]),
-// k / v into the cache row of position pos.
+// k / v into cache row crow (the position, or its paged slot).
 template <int D, int QDT, int KVDT>
 __device__ __forceinline__ void store_head(const float (&x)[D / 64], int kind, int head, int row,
-                                           int pos, int e0, int64_t q_dim, void *q_out,
+                                           int64_t crow, int e0, int64_t q_dim, void *q_out,
                                            void *k_cache, void *v_cache, int64_t kv_stride) {
     constexpr int E = D / 64;
     if (kind == 0)
         store_e<QDT, E>(q_out, row * q_dim + (int64_t)head * D + e0, x);
     else
         store_e<KVDT, E>(kind == 1 ? k_cache : v_cache,
-                         (int64_t)pos * kv_stride + (int64_t)head * D + e0, x);
+                         crow * kv_stride + (int64_t)head * D + e0, x);
 }
+
+// Paged destination of the K/V rows (pos == nullptr: the contiguous cache,
+// row r at position start_pos + r).  Row r of a paged call is one token of
+// sequence r at position pos[r], stored in slot pos % P of page
+// tab[r * stride + pos / P] (P = 2^shift); a row whose position falls
+// outside [0, rope_n_pos) or whose page index is outside the table or the
+// pool is skipped (nothing written).
+struct PageMap {
+    const int32_t *pos, *tab;
+    int stride, shift, n_pages, rope_n_pos;
+};
 
 template <int D, int QDT, int KVDT>
 __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
@@ -169,14 +180,23 @@ __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
     const float *__restrict__ v_bias, const float *__restrict__ q_norm,
     const float *__restrict__ k_norm, float eps, const float *__restrict__ cs, int neox,
     int rotary_dim, int rows, int start_pos, int n_head, int n_kv_head, void *q_out,
-    void *k_cache, void *v_cache, int64_t kv_stride) {
+    void *k_cache, void *v_cache, int64_t kv_stride, PageMap pm) {
     constexpr int E = D / 64;
     __shared__ float buf[kAppendWaves][D];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: slot math in SGPRs
     const int row = blockIdx.x;
     const int slots = n_head + 2 * n_kv_head;
     const int64_t q_dim = (int64_t)n_head * D, kv_dim = (int64_t)n_kv_head * D;
-    const int pos = start_pos + row;
+    int pos = start_pos + row;
+    int64_t crow = pos;
+    if (pm.pos) {  // wave-uniform
+        pos = __builtin_amdgcn_readfirstlane(pm.pos[row]);
+        const int pg = pos >> pm.shift;
+        const bool in = pos >= 0 && pos < pm.rope_n_pos && pg < pm.stride;
+        const int phys = in ? __builtin_amdgcn_readfirstlane(pm.tab[(int64_t)row * pm.stride + pg]) : -1;
+        if (phys < 0 || phys >= pm.n_pages) return;
+        crow = ((int64_t)phys << pm.shift) + (pos & ((1 << pm.shift) - 1));
+    }
     const HeadEpi<D> epi(cs, pos, rotary_dim, neox, q_norm, k_norm, eps);
     const int e0 = epi.e0;
 
@@ -206,7 +226,7 @@ __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
 #pragma unroll
             for (int i = 0; i < E; i++) x[b][i] += bv[b][i];
             epi.norm_rope(x[b], kind[b], buf[wave]);
-            store_head<D, QDT, KVDT>(x[b], kind[b], head[b], row, pos, e0, q_dim, q_out, k_cache,
+            store_head<D, QDT, KVDT>(x[b], kind[b], head[b], row, crow, e0, q_dim, q_out, k_cache,
                                      v_cache, kv_stride);
         }
     }
@@ -351,7 +371,7 @@ __global__ __launch_bounds__(kProjWaves * 64) void qkv_proj_kernel(
         for (int i = 0; i < E; i++) v[i] += bv[i];
     }
     epi.norm_rope(v, kind, lrow);
-    store_head<D, QDT, KVDT>(v, kind, head, row, pos, epi.e0, (int64_t)n_head * D, q_out,
+    store_head<D, QDT, KVDT>(v, kind, head, row, (int64_t)pos, epi.e0, (int64_t)n_head * D, q_out,
                              k_cache, v_cache, kv_stride);
 }
 
@@ -360,13 +380,13 @@ static void launch_kv(int kvdt, dim3 g, dim3 b, hipStream_t st, const float *qi,
                       const float *vi, const float *qb, const float *kb, const float *vb,
                       const float *qn, const float *kn, float eps, const float *cs, int neox,
                       int rd, int rows, int sp, int nh, int nkv, void *qo, void *kc, void *vc,
-                      int64_t kvs) {
+                      int64_t kvs, PageMap pm) {
     if (kvdt == ULLM_DT_F32)
-        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_F32>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs);
+        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_F32>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
     else if (kvdt == ULLM_DT_F16)
-        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_F16>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs);
+        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_F16>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
     else
-        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_BF16>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs);
+        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_BF16>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
 }
 
 template <int D>
@@ -374,10 +394,10 @@ static void launch_q(int qdt, int kvdt, dim3 g, dim3 b, hipStream_t st, const fl
                      const float *ki, const float *vi, const float *qb, const float *kb,
                      const float *vb, const float *qn, const float *kn, float eps,
                      const float *cs, int neox, int rd, int rows, int sp, int nh, int nkv,
-                     void *qo, void *kc, void *vc, int64_t kvs) {
-    if (qdt == ULLM_DT_F32) launch_kv<D, ULLM_DT_F32>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs);
-    else if (qdt == ULLM_DT_F16) launch_kv<D, ULLM_DT_F16>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs);
-    else launch_kv<D, ULLM_DT_BF16>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs);
+                     void *qo, void *kc, void *vc, int64_t kvs, PageMap pm) {
+    if (qdt == ULLM_DT_F32) launch_kv<D, ULLM_DT_F32>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
+    else if (qdt == ULLM_DT_F16) launch_kv<D, ULLM_DT_F16>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
+    else launch_kv<D, ULLM_DT_BF16>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
 }
 
 }  // namespace ullm
@@ -436,11 +456,55 @@ extern "C" int ullm_hip_qkv_append(const float *q_in, const float *k_in, const f
     dim3 grid((unsigned)rows), block(kAppendWaves * 64);
     hipStream_t st = (hipStream_t)stream;
     switch (head_dim) {
-        case 64: launch_q<64>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride); break;
-        case 128: launch_q<128>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride); break;
-        default: launch_q<256>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride); break;
+        case 64: launch_q<64>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride, PageMap{}); break;
+        case 128: launch_q<128>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride, PageMap{}); break;
+        default: launch_q<256>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride, PageMap{}); break;
     }
     return check_hip(hipGetLastError(), "qkv_append launch");
+}
+
+extern "C" int ullm_hip_qkv_append_paged(const float *q_in, const float *k_in, const float *v_in,
+                                         const float *q_bias, const float *k_bias,
+                                         const float *v_bias, const float *q_norm,
+                                         const float *k_norm, float eps, const float *rope_cs,
+                                         int rope_n_pos, int rope_neox, int rotary_dim, int rows,
+                                         const int32_t *positions, int n_head, int n_kv_head,
+                                         int head_dim, void *q_out, int q_dtype, void *k_pages,
+                                         void *v_pages, int kv_dtype, int64_t kv_stride,
+                                         int page_size, int n_pages, const int32_t *block_table,
+                                         int table_stride, void *stream) {
+    if (!dtype_ok(q_dtype) || !dtype_ok(kv_dtype))
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "qkv_append_paged: dtype q=%d kv=%d", q_dtype, kv_dtype);
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "qkv_append_paged: head_dim %d not in {64,128,256}",
+                         head_dim);
+    if (rows < 0 || rows > 0x7fffffff / 4 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_append_paged: bad rows/heads");
+    if (rotary_dim < 2 || rotary_dim > head_dim || (rotary_dim & 1))
+        return set_error(ULLM_HIP_E_INVALID, "qkv_append_paged: rotary_dim %d", rotary_dim);
+    if (kv_stride < (int64_t)n_kv_head * head_dim)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_append_paged: kv_stride too small");
+    if (page_size < 1 || (page_size & (page_size - 1)))
+        return set_error(ULLM_HIP_E_INVALID, "qkv_append_paged: page_size %d must be a power of two",
+                         page_size);
+    if (n_pages < 1 || table_stride < 1 || rope_n_pos < 1)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_append_paged: n_pages/table_stride/rope_n_pos < 1");
+    if (rows == 0) return ULLM_HIP_OK;
+    if (!q_in || !k_in || !v_in || !rope_cs || !q_out || !k_pages || !v_pages || !positions ||
+        !block_table)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_append_paged: null tensor pointer");
+    if (q_out == (void *)q_in && q_dtype != ULLM_DT_F32)
+        return set_error(ULLM_HIP_E_INVALID, "qkv_append_paged: in-place q needs q_dtype f32");
+    const PageMap pm{positions, block_table, table_stride, __builtin_ctz(page_size), n_pages,
+                     rope_n_pos};
+    dim3 grid((unsigned)rows), block(kAppendWaves * 64);
+    hipStream_t st = (hipStream_t)stream;
+    switch (head_dim) {
+        case 64: launch_q<64>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, 0, n_head, n_kv_head, q_out, k_pages, v_pages, kv_stride, pm); break;
+        case 128: launch_q<128>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, 0, n_head, n_kv_head, q_out, k_pages, v_pages, kv_stride, pm); break;
+        default: launch_q<256>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, 0, n_head, n_kv_head, q_out, k_pages, v_pages, kv_stride, pm); break;
+    }
+    return check_hip(hipGetLastError(), "qkv_append_paged launch");
 }
 
 namespace ullm {
