@@ -154,6 +154,45 @@ def bench_prefill(torch, A, args, S, H, Hk, D, dt):
     return dict(ms=ms, tflops=flop / (ms * 1e-3) / 1e12, flop=flop, launches=n)
 
 
+def bench_prefill_paged(torch, A, args, S, H, Hk, D, dt, page):
+    """cfg3 prefill with K/V in pages of `page` positions shuffled over a
+    pool (chunked-prefill layout), timed like bench_prefill."""
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(99)
+    q = torch.randn(S, H * D, generator=g, device=dev).to(dt)
+    n_pages = (S + page - 1) // page
+    kp = torch.randn(n_pages, page, Hk * D, generator=g, device=dev).to(dt)
+    vp = torch.randn(n_pages, page, Hk * D, generator=g, device=dev).to(dt)
+    table = torch.randperm(n_pages, generator=g, device=dev).to(torch.int32)
+    out = torch.empty(S, H * D, device=dev)
+    run = lambda: A.attn_prefill_paged(q, kp, vp, table, H, Hk, D, out=out)  # noqa: E731
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    reps = 20
+    gr = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(gr, stream=st):
+            for _ in range(reps):
+                run()
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    gr.replay()
+    torch.cuda.synchronize()
+    n = max(3, min(args.steps // 20, 20))
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(n):
+        gr.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / (n * reps)
+    flop = 4.0 * D * H * S * (S + 1) / 2
+    return dict(ms=ms, tflops=flop / (ms * 1e-3) / 1e12, page=page)
+
+
 def bench_append(torch, A, args, S, H, Hk, D, dt):
     """cfg3's fused append: S rows of f32 q/k/v -> Q/K RMSNorm -> NeoX RoPE
     (theta 1e6) -> q (bf16) and the K/V cache rows (bf16).  HBM-bound: the
@@ -451,6 +490,8 @@ def main():
         res["cfg2"] = bench_decode(torch, A, args, 12, 2, 128, 4096, 28, torch.float16, "cfg2")
     if args.only in ("all", "prefill"):
         res["cfg3"] = bench_prefill(torch, A, args, 2048, 32, 8, 128, torch.bfloat16)
+        res["cfg3_paged"] = bench_prefill_paged(torch, A, args, 2048, 32, 8, 128, torch.bfloat16,
+                                                256)
     if args.only in ("all", "append"):
         res["append"] = bench_append(torch, A, args, 2048, 32, 8, 128, torch.bfloat16)
     if args.only in ("all", "proj"):
@@ -496,7 +537,10 @@ def main():
         "prefill": {"workload": "cfg3 Qwen3-4B-shaped causal prefill, S=2048, 32/8 heads, "
                                 "head_dim 128, bf16", "ms": round(p["ms"], 4),
                     "tflops": round(p["tflops"], 2),
-                    "flop_causal": p["flop"]},
+                    "flop_causal": p["flop"],
+                    "paged": {"page": res["cfg3_paged"]["page"],
+                              "ms": round(res["cfg3_paged"]["ms"], 4),
+                              "tflops": round(res["cfg3_paged"]["tflops"], 2)}},
         "long_decode": {"workload": "cfg5 Qwen3-30B-A3B-shaped decode, 32/4 heads, head_dim "
                                     "128, bf16 KV 32768, 48 layers",
                         "us_per_layer": round(lc["us_per_layer"], 3),

@@ -225,6 +225,22 @@ int ullm_hip_qkv_append_paged(const float *q_in, const float *k_in, const float 
                               int kv_dtype, int64_t kv_stride, int page_size, int n_pages,
                               const int32_t *block_table, int table_stride, void *stream);
 
+/* Causal prefill attention whose keys live in a PAGED cache: the S query
+ * rows are positions start_pos..start_pos+S-1 of one sequence, and key t of
+ * that sequence is slot t % page_size of page block_table[t / page_size]
+ * (the layout of ullm_hip_attn_decode_paged; DEVICE int32[table_len],
+ * table_len * page_size >= start_pos + S).  Same result as
+ * ullm_hip_attn_prefill on the gathered cache: chunked prefill of a
+ * sequence whose earlier positions are already in pages.  No counterpart in
+ * the reference (contiguous cache, lib.rs:184-185).  page_size: a power of
+ * two >= 64; head_dim 64 or 128 (else ULLM_HIP_E_UNSUPPORTED); f16/bf16.
+ * Pages outside [0, n_pages) read as zeros. */
+int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, const void *v_pages,
+                                int dtype, int64_t kv_stride, int page_size, int n_pages,
+                                const int32_t *block_table, int table_len, int s, int start_pos,
+                                int window, int n_head, int n_kv_head, int head_dim, float scale,
+                                float *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

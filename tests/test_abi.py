@@ -179,3 +179,22 @@ def test_paged_append_validation():
     assert call(npages=0) == L.E_INVALID
     assert call(rows=0) == L.OK
     assert call() == L.E_INVALID  # null pointers
+
+
+def test_paged_prefill_validation():
+    f = L.lib().ullm_hip_attn_prefill_paged
+
+    def call(**kw):
+        a = dict(q=None, kp=None, vp=None, dt=L.DT_BF16, kvs=1024, page=64, npages=10, tab=None,
+                 tl=40, s=512, sp=0, win=0, h=32, hk=8, d=128, sc=0.1, out=None, st=None)
+        a.update(kw)
+        return f(*a.values())
+
+    assert call(dt=L.DT_F32) == L.E_UNSUPPORTED
+    assert call(d=256) == L.E_UNSUPPORTED
+    assert call(page=32) == L.E_INVALID   # below one 64-key tile
+    assert call(page=96) == L.E_INVALID
+    assert call(tl=7) == L.E_INVALID      # 7 pages < 512 positions
+    assert call(hk=3) == L.E_INVALID
+    assert call(s=0) == L.OK
+    assert call() == L.E_INVALID  # null pointers

@@ -237,3 +237,47 @@ def test_paged_serving_loop(dev):
             ref = ora.attn_decode(qo[b].cpu().numpy().copy(), kr, vr, n - 1, H, Hk, D,
                                   1.0 / math.sqrt(D))
             assert_close(out[b].cpu().numpy().reshape(-1), ref, what=f"step {step} b={b}")
+
+
+PREFILL_CASES = [
+    # (S, start_pos, H, Hk, D, dtype, page, window)
+    (300, 0, 8, 2, 128, "bf16", 64, 0),
+    (200, 700, 32, 8, 128, "bf16", 128, 0),     # chunked prefill over earlier pages
+    (150, 1000, 12, 2, 64, "f16", 64, 300),     # binding window (prefill2 path)
+    (1, 63, 8, 8, 128, "f16", 64, 0),           # one row at a page edge
+    (2048, 0, 32, 8, 128, "bf16", 256, 0),      # cfg3 shape
+]
+
+
+@pytest.mark.parametrize("case", range(len(PREFILL_CASES)))
+def test_paged_prefill(dev, case):
+    """ullm_hip_attn_prefill_paged equals ullm_hip_attn_prefill on the
+    gathered cache bit for bit (same kernels and tiles; rows past the length
+    read as zeros either way), and the oracle on sampled rows; unused slots
+    hold NaN."""
+    S, sp, H, Hk, D, dt, page, window = PREFILL_CASES[case]
+    print(f"[paged-prefill] S{S} sp{sp} H{H} Hk{Hk} D{D} {dt} page{page} win{window}", flush=True)
+    n = sp + S
+    kvs = Hk * D
+    kc = synth.randn(case, 2, (n, kvs), DT[dt]).to(dev)
+    vc = synth.randn(case, 3, (n, kvs), DT[dt]).to(dev)
+    q = synth.randn(case, 1, (S, H * D), DT[dt]).to(dev)
+    n_used = (n + page - 1) // page
+    n_pages = n_used + 3
+    perm = np.random.default_rng(case).permutation(n_pages)[:n_used]
+    kp = torch.full((n_pages, page, kvs), float("nan"), dtype=DT[dt], device=dev)
+    vp = torch.full_like(kp, float("nan"))
+    for pg in range(n_used):
+        r = min(page, n - pg * page)
+        kp[perm[pg], :r] = kc[pg * page:pg * page + r]
+        vp[perm[pg], :r] = vc[pg * page:pg * page + r]
+    table = torch.tensor(list(perm) + [-1], dtype=torch.int32, device=dev)
+    out = A.attn_prefill_paged(q, kp, vp, table, H, Hk, D, start_pos=sp, window=window)
+    ref_c = A.attn_prefill(q, kc, vc, H, Hk, D, start_pos=sp, window=window)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_c), f"case {case}: paged != contiguous bits"
+    rows = sorted({0, S - 1, S // 2, min(31, S - 1), min(64, S - 1)})
+    ref = ora.attn_prefill(q.float().cpu().numpy(), kc.float().cpu().numpy(),
+                           vc.float().cpu().numpy(), S, sp, H, Hk, D, 1.0 / math.sqrt(D),
+                           window=window, rows=rows)
+    assert_close(out.cpu().numpy()[rows], ref[rows], what=f"case {case}")

@@ -39,6 +39,9 @@ SIGNATURES = {
     ),
     "ullm_hip_qkv_proj_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "ullm_hip_matmul": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp]),
+    "ullm_hip_attn_prefill_paged": (
+        _i, [_vp, _vp, _vp, _i, _i64, _i, _i, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _vp, _vp]
+    ),
     "ullm_hip_qkv_append_paged": (
         _i,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _i, _vp, _i, _i, _i, _vp,

@@ -154,6 +154,32 @@ def qkv_append_paged(q, k, v, k_pages, v_pages, rope_cs, positions, block_table,
     return q_out
 
 
+def attn_prefill_paged(q, k_pages, v_pages, block_table, n_head, n_kv_head, head_dim, *,
+                       start_pos=0, window=0, scale=None, out=None, stream=None):
+    """Causal prefill of S rows (positions start_pos..) of one sequence whose
+    keys live in pages: block_table int32 [table_len] (page of key t =
+    block_table[t // page_size]).  q: [S, n_head*head_dim] f16/bf16."""
+    S = q.shape[0]
+    _need_cuda(q, k_pages, v_pages, block_table)
+    if not q.is_contiguous() or q.numel() != S * n_head * head_dim:
+        raise L.UllmHipError(L.E_INVALID, "q must be contiguous [S, n_head*head_dim]")
+    if k_pages.dim() != 3 or k_pages.shape != v_pages.shape or q.dtype != k_pages.dtype:
+        raise L.UllmHipError(L.E_INVALID, "k_pages/v_pages must be [n_pages, page_size, kv_stride] of q's dtype")
+    if block_table.dtype != torch.int32 or block_table.dim() != 1:
+        raise L.UllmHipError(L.E_INVALID, "block_table must be int32 [table_len]")
+    n_pages, page_size, kv_stride = k_pages.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    if out is None:
+        out = torch.empty(S, n_head * head_dim, dtype=torch.float32, device=q.device)
+    rc = L.lib().ullm_hip_attn_prefill_paged(
+        _ptr(q), _ptr(k_pages), _ptr(v_pages), _dt(q), kv_stride, page_size, n_pages,
+        _ptr(block_table), block_table.numel(), S, start_pos, window, n_head, n_kv_head, head_dim,
+        float(scale), _ptr(out), _stream(stream))
+    L.check(rc)
+    return out
+
+
 def attn_prefill(q, k_cache, v_cache, n_head, n_kv_head, head_dim, *, start_pos=0, window=0,
                  scale=None, kv_stride=None, out=None, stream=None):
     """Causal prefill attention on MFMA (lib.rs:1061-1087).

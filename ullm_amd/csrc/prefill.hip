@@ -83,11 +83,39 @@ struct PF2 {
     static_assert(NIW >= 1 && NI % NW == 0, "DMA split");
 };
 
+// Paged K/V (tab == nullptr: the contiguous cache).  Key t of the sequence
+// is row t % P of page tab[t / P] (P = 2^shift, a multiple of the 64-key
+// tile), so a tile's DMA goes through a buffer resource based at its page
+// whose range ends at the sequence length: rows past it, and pages outside
+// the table or [0, n_pages), read as zeros.
+struct KvPages {
+    const int32_t *tab;
+    int tab_len, shift, n_pages;
+};
+
+// Buffer resources and scalar offset of the 64-key tile starting at key0.
+template <int D>
+__device__ __forceinline__ void page_tile(const KvPages &pg, const char *kc, const char *vc,
+                                          int kvh, int rbg, int kv_len, int key0,
+                                          __amdgpu_buffer_rsrc_t &kr, __amdgpu_buffer_rsrc_t &vr,
+                                          int &so) {
+    const int pi = key0 >> pg.shift;
+    const int phys = key0 < kv_len && pi < pg.tab_len ? pg.tab[pi] : -1;
+    const bool ok = phys >= 0 && phys < pg.n_pages;
+    const int64_t pb = ((int64_t)(ok ? phys : 0) << pg.shift) * rbg + (int64_t)kvh * D * 2;
+    const int rows = min(1 << pg.shift, kv_len - (pi << pg.shift));
+    const int range = ok ? (rows - 1) * rbg + D * 2 : 0;
+    kr = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + pb), 0, range, kRsrcWord3);
+    vr = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + pb), 0, range, kRsrcWord3);
+    so = __builtin_amdgcn_readfirstlane((key0 & ((1 << pg.shift) - 1)) * rbg);
+}
+
 template <class T, int D>
 __global__ __launch_bounds__(512) void prefill2_kernel(
     const uint16_t *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int S, int start_pos, int window, int n_head, int kv_mul, int hw,
-    int rw, int n_units, int ng, int np, int paired, float qscale, float *__restrict__ out) {
+    int rw, int n_units, int ng, int np, int paired, float qscale, float *__restrict__ out,
+    KvPages pgs) {
     using C = PF2<D>;
     constexpr int BN = C::BN, RB = C::RB, SLOTS = C::SLOTS, RPI = C::RPI, NIW = C::NIW;
     constexpr int TILE = C::TILE, STAGE = C::STAGE, NKT = C::NKT, NKS = C::NKS, NDT = C::NDT;
@@ -151,12 +179,15 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
     const int kt0 = hi > 0 ? (max(lo, 0) / BN) : 0;
     const int nt = hi > 0 ? (hi + BN - 1) / BN - kt0 : 0;
     auto issue = [&](int tt) {
-        const int so = __builtin_amdgcn_readfirstlane((kt0 + tt) * BN * rbg);
+        __amdgpu_buffer_rsrc_t kr = krs, vr = vrs;
+        int so;
+        if (pgs.tab) page_tile<D>(pgs, kc, vc, kvh, rbg, kv_len, (kt0 + tt) * BN, kr, vr, so);
+        else so = __builtin_amdgcn_readfirstlane((kt0 + tt) * BN * rbg);
         char *st = lds + (tt % C::NSTG) * STAGE;
 #pragma unroll
         for (int i = 0; i < NIW; i++) {
-            dma16(krs, st + (wave * NIW + i) * 1024, dofs[i] + so, 0);
-            dma16(vrs, st + TILE + (wave * NIW + i) * 1024, dofs[i] + so, 0);
+            dma16(kr, st + (wave * NIW + i) * 1024, dofs[i] + so, 0);
+            dma16(vr, st + TILE + (wave * NIW + i) * 1024, dofs[i] + so, 0);
         }
     };
 
@@ -370,7 +401,7 @@ template <class T, int D>
 __global__ __launch_bounds__(512) void prefill4_kernel(
     const uint16_t *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int S, int start_pos, int n_head, int kv_mul, int lhw, int ng, int np,
-    float qscale, float *__restrict__ out) {
+    float qscale, float *__restrict__ out, KvPages pgs) {
     using C = PF2<D>;
     constexpr int BN = C::BN, RB = C::RB, SLOTS = C::SLOTS, RPI = C::RPI, NIW = C::NIW;
     constexpr int TILE = C::TILE, NKT = C::NKT, NKS = C::NKS, NDT = C::NDT;
@@ -445,13 +476,28 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
         const int r = (slot * NIWS + i) * RPI + lane / SLOTS;
         dofs[i] = r * rbg + (((lane % SLOTS) ^ swz(r)) * 16);
     }
+    // Paged: buffer resources of the items in flight, by item parity.
+    struct PageSlot { __amdgpu_buffer_rsrc_t k, v; int so; };
+    PageSlot pslot[2] = {{krs, vrs, 0}, {krs, vrs, 0}};
     // This wave's chunks of item i of its set's stream: K (kv = 0) or V (kv = 1).
     auto load_tile = [&](int kv, int i) {
         const int t = i < n_me ? item_tile(set, i) : (kv_len + BN) / BN;  // past: zeros
-        const int so = t * BN * rbg;
+        __amdgpu_buffer_rsrc_t kr = krs, vr = vrs;
+        int so;
+        if (pgs.tab) {
+            // The page of item i is looked up once, when its K goes out; its
+            // V (one step later) reuses it from the item's parity slot.
+            PageSlot &ps = (i & 1) ? pslot[1] : pslot[0];
+            if (kv == 0) page_tile<D>(pgs, kc, vc, kvh, rbg, kv_len, t * BN, ps.k, ps.v, ps.so);
+            kr = ps.k;
+            vr = ps.v;
+            so = ps.so;
+        } else {
+            so = t * BN * rbg;
+        }
         char *st = lds + kv * VREG + (2 * (i & 1) + set) * TILE + slot * NIWS * 1024;
 #pragma unroll
-        for (int c = 0; c < NIWS; c++) dma16(kv ? vrs : krs, st + c * 1024, dofs[c] + so, 0);
+        for (int c = 0; c < NIWS; c++) dma16(kv ? vr : kr, st + c * 1024, dofs[c] + so, 0);
     };
     // bf16 -> f16 in place, for the V chunks this wave loaded of item j + 1.
     auto widen_own = [&](int j) {
@@ -1096,13 +1142,14 @@ struct PrefillLaunch {
 template <class T, int D>
 struct PrefillLaunch<T, D, true> {
     static void run(const void *q, const void *kc, const void *vc, int64_t kvs, int S, int sp,
-                    int win, int nh, int kv_mul, float qs, float *out, hipStream_t st);
+                    int win, int nh, int kv_mul, float qs, float *out, hipStream_t st,
+                    KvPages pgs = KvPages{});
 };
 
 template <class T, int D>
 void PrefillLaunch<T, D, true>::run(const void *q, const void *kc, const void *vc, int64_t kvs,
                                     int S, int sp, int win, int nh, int kv_mul, float qs,
-                                    float *out, hipStream_t st) {
+                                    float *out, hipStream_t st, KvPages pgs) {
     // Units of HW heads (HW | kv_mul, at most 4) x groups of RW = 4/HW 32-row blocks.
     const int hw = kv_mul % 4 == 0 ? 4 : (kv_mul % 2 == 0 ? 2 : 1);
     const int rw = 4 / hw;
@@ -1118,12 +1165,12 @@ void PrefillLaunch<T, D, true>::run(const void *q, const void *kc, const void *v
         const int lhw = hw == 4 ? 2 : (hw == 2 ? 1 : 0);
         hipLaunchKernelGGL((prefill4_kernel<T, D>), dim3(per_xcd * 8), dim3(512), 0, st,
                            (const uint16_t *)q, (const char *)kc, (const char *)vc, kvs, S, sp,
-                           nh, kv_mul, lhw, ng, np, qs, out);
+                           nh, kv_mul, lhw, ng, np, qs, out, pgs);
         return;
     }
     hipLaunchKernelGGL((prefill2_kernel<T, D>), dim3(per_xcd * 8), dim3(512), 0, st,
                        (const uint16_t *)q, (const char *)kc, (const char *)vc, kvs, S, sp, win,
-                       nh, kv_mul, hw, rw, n_units, ng, np, paired, qs, out);
+                       nh, kv_mul, hw, rw, n_units, ng, np, paired, qs, out, pgs);
 }
 
 template <class T, int D>
@@ -1175,3 +1222,48 @@ extern "C" int ullm_hip_attn_prefill(const void *q, const void *k_cache, const v
         return dispatch_prefill<BF16>(head_dim, q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
     return dispatch_prefill<F16>(head_dim, q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
 }
+
+extern "C" int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, const void *v_pages,
+                                           int dtype, int64_t kv_stride, int page_size,
+                                           int n_pages, const int32_t *block_table,
+                                           int table_len, int S, int start_pos, int window,
+                                           int n_head, int n_kv_head, int head_dim, float scale,
+                                           float *out, void *stream) {
+    if (dtype != ULLM_DT_F16 && dtype != ULLM_DT_BF16)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: dtype %d (f16/bf16)", dtype);
+    if (head_dim != 64 && head_dim != 128)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: head_dim %d not in {64,128}", head_dim);
+    if (n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || S < 0 || start_pos < 0)
+        return set_error(ULLM_HIP_E_INVALID, "prefill_paged: bad shape S=%d start_pos=%d heads=%d/%d",
+                         S, start_pos, n_head, n_kv_head);
+    if (kv_stride < (int64_t)n_kv_head * head_dim || (kv_stride * 2) % 16)
+        return set_error(ULLM_HIP_E_INVALID,
+                         "prefill_paged: kv_stride must be >= n_kv_head*head_dim and 16-byte aligned");
+    if (page_size < 64 || (page_size & (page_size - 1)))
+        return set_error(ULLM_HIP_E_INVALID, "prefill_paged: page_size %d must be a power of two >= 64",
+                         page_size);
+    if ((int64_t)page_size * kv_stride * 2 > 0x7fff0000LL)
+        return set_error(ULLM_HIP_E_INVALID, "prefill_paged: a page exceeds 2 GiB");
+    if (n_pages < 1) return set_error(ULLM_HIP_E_INVALID, "prefill_paged: n_pages %d < 1", n_pages);
+    if ((int64_t)table_len * page_size < (int64_t)start_pos + S)
+        return set_error(ULLM_HIP_E_INVALID, "prefill_paged: table of %d pages holds fewer than %d positions",
+                         table_len, start_pos + S);
+    if (S == 0) return ULLM_HIP_OK;
+    if (!q || !k_pages || !v_pages || !block_table || !out)
+        return set_error(ULLM_HIP_E_INVALID, "prefill_paged: null tensor pointer");
+    if (((uintptr_t)q | (uintptr_t)k_pages | (uintptr_t)v_pages | (uintptr_t)out) & 15)
+        return set_error(ULLM_HIP_E_INVALID, "prefill_paged: tensors must be 16-byte aligned");
+    const KvPages pgs{block_table, table_len, __builtin_ctz(page_size), n_pages};
+    const float qs = scale * kLog2e;
+    const int kv_mul = n_head / n_kv_head;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == ULLM_DT_BF16) {
+        if (head_dim == 64) PrefillLaunch<BF16, 64>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
+        else PrefillLaunch<BF16, 128>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
+    } else {
+        if (head_dim == 64) PrefillLaunch<F16, 64>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
+        else PrefillLaunch<F16, 128>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
+    }
+    return check_hip(hipGetLastError(), "prefill_paged launch");
+}
+
