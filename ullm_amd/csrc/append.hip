@@ -340,23 +340,31 @@ __global__ __launch_bounds__(kProjWaves * 64) void qkv_proj_kernel(
     if (wave != 0) return;
     if constexpr (NSP > 1) {
         // NSP workgroups share a head vector: wave 0 of each stores its part
-        // to the workspace and counts itself in (agent-scope acquire-release:
-        // the wait for the wave's stores and the L2 write-back come with the
-        // release); the last to arrive reads the whole vector back, finishes
-        // the head and resets the counter for the next call.
+        // to the workspace and counts itself in; the last to arrive reads
+        // the whole vector back, finishes the head and resets the counter
+        // for the next call.  The parts travel by system-coherent accesses
+        // (sc0 sc1: stores written through to memory, loads served from
+        // it), so no L2 write-back or invalidate is needed: each part's
+        // stores have completed (vmcnt(0)) before its counter increment, and
+        // the last arriver's loads bypass its XCD's L2.  An agent-scope
+        // acquire-release counter (L2 write-back and invalidate) measured
+        // 12.4 us against 10.9 us at the Qwen3-4B decode shape.
         constexpr int PART = D / NSP;
         float *yh = ws_y + ((int64_t)row * slots + slot) * D;
-        for (int i = lane; i < PART; i += 64) yh[part * PART + i] = ys[part * PART + i];
+        for (int i = lane; i < PART; i += 64)
+            __hip_atomic_store(yh + part * PART + i, ys[part * PART + i], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         uint32_t prev = 0;
         if (lane == 0) {
             uint32_t *cnt = ws_cnt + (int64_t)row * slots + slot;
-            prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (prev == NSP - 1) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         prev = __builtin_amdgcn_readfirstlane(prev);
         if (prev != NSP - 1) return;
         for (int i = lane; i < D; i += 64)
-            ys[i] = __hip_atomic_load(yh + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ys[i] = __hip_atomic_load(yh + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         __builtin_amdgcn_wave_barrier();
     }
     const int pos = start_pos + row;
