@@ -191,7 +191,7 @@ def test_paged_prefill_validation():
         return f(*a.values())
 
     assert call(dt=L.DT_F32) == L.E_UNSUPPORTED
-    assert call(d=256) == L.E_UNSUPPORTED
+    assert call(d=96) == L.E_UNSUPPORTED
     assert call(page=32) == L.E_INVALID   # below one 64-key tile
     assert call(page=96) == L.E_INVALID
     assert call(tl=7) == L.E_INVALID      # 7 pages < 512 positions

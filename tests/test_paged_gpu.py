@@ -246,6 +246,8 @@ PREFILL_CASES = [
     (150, 1000, 12, 2, 64, "f16", 64, 300),     # binding window (prefill2 path)
     (1, 63, 8, 8, 128, "f16", 64, 0),           # one row at a page edge
     (2048, 0, 32, 8, 128, "bf16", 256, 0),      # cfg3 shape
+    (1024, 0, 8, 4, 256, "f16", 64, 0),         # head_dim 256 (split-K kernel), cfg4 shape
+    (300, 900, 8, 4, 256, "bf16", 128, 500),    # head_dim 256, chunked, binding window
 ]
 
 

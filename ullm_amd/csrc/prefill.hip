@@ -864,7 +864,7 @@ template <class T, int D>
 __global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
     const uint16_t *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int S, int start_pos, int window, int n_head, int kv_mul, int nb,
-    float qscale, float *__restrict__ out) {
+    float qscale, float *__restrict__ out, KvPages pgs) {
     constexpr int BN = 32, RB = D * 2, SLOTS = D / 8, RPI = 1024 / RB, NI = BN / RPI;
     constexpr int TILE = BN * RB;  // bytes of one V tile
     constexpr int NKS = D / 16, NDT = D / 32, CPW = D / 16;
@@ -924,20 +924,31 @@ __global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
     // this wave's range is addressed past the buffer range, which reads
     // zero without touching memory, as do keys past the cache's end.
     auto tile_off = [&](int t) { return __builtin_amdgcn_readfirstlane(t < tb ? t * BN * rbg : range); };
+    // Paged: the tile's page resources (a dead tile addresses the sequence
+    // end, past every page's range).
+    auto page_of = [&](int t, __amdgpu_buffer_rsrc_t &kp, __amdgpu_buffer_rsrc_t &vp, int &so) {
+        page_tile<D>(pgs, kc, vc, kvh, rbg, kv_len, t < tb ? t * BN : kv_len, kp, vp, so);
+    };
     auto issue_k = [&](u32x4(&kr)[NKS], int t) {
-        const int so = tile_off(t);
+        __amdgpu_buffer_rsrc_t kp = krs, vp = vrs;
+        int so;
+        if (pgs.tab) page_of(t, kp, vp, so);
+        else so = tile_off(t);
 #pragma unroll
         for (int s = 0; s < NKS; s++)
             kr[s] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff + s * 32 + so, 0, 0));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(kp, koff + s * 32 + so, 0, 0));
         __builtin_amdgcn_sched_barrier(0);  // keep the K loads ahead of later V requests
     };
     auto issue_v = [&](int st, int t) {
-        const int so = tile_off(t);
+        __amdgpu_buffer_rsrc_t kp = krs, vp = vrs;
+        int so;
+        if (pgs.tab) page_of(t, kp, vp, so);
+        else so = tile_off(t);
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int r = i * RPI + lr;
-            dma16(vrs, vst + st * TILE + i * 1024, r * rbg + ((slot ^ swz(r)) * 16) + so, 0);
+            dma16(vp, vst + st * TILE + i * 1024, r * rbg + ((slot ^ swz(r)) * 16) + so, 0);
         }
     };
     // bf16 -> f16 in place, for the chunks this lane's DMA wrote.
@@ -1130,13 +1141,14 @@ __global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
 template <class T, int D, bool V2 = (D <= 128)>
 struct PrefillLaunch {
     static void run(const void *q, const void *kc, const void *vc, int64_t kvs, int S, int sp,
-                    int win, int nh, int kv_mul, float qs, float *out, hipStream_t st) {
+                    int win, int nh, int kv_mul, float qs, float *out, hipStream_t st,
+                    KvPages pgs = KvPages{}) {
         const int nb = (S + 31) / 32;
         const int total = nh * nb;
         const int per_xcd = (total + 7) / 8;
         hipLaunchKernelGGL((prefill_sk_kernel<T, D>), dim3(per_xcd * 8), dim3(256), 0, st,
                            (const uint16_t *)q, (const char *)kc, (const char *)vc, kvs, S, sp,
-                           win, nh, kv_mul, nb, qs, out);
+                           win, nh, kv_mul, nb, qs, out, pgs);
     }
 };
 template <class T, int D>
@@ -1231,8 +1243,8 @@ extern "C" int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, c
                                            float *out, void *stream) {
     if (dtype != ULLM_DT_F16 && dtype != ULLM_DT_BF16)
         return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: dtype %d (f16/bf16)", dtype);
-    if (head_dim != 64 && head_dim != 128)
-        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: head_dim %d not in {64,128}", head_dim);
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: head_dim %d not in {64,128,256}", head_dim);
     if (n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || S < 0 || start_pos < 0)
         return set_error(ULLM_HIP_E_INVALID, "prefill_paged: bad shape S=%d start_pos=%d heads=%d/%d",
                          S, start_pos, n_head, n_kv_head);
@@ -1259,10 +1271,12 @@ extern "C" int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, c
     hipStream_t st = (hipStream_t)stream;
     if (dtype == ULLM_DT_BF16) {
         if (head_dim == 64) PrefillLaunch<BF16, 64>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
-        else PrefillLaunch<BF16, 128>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
+        else if (head_dim == 128) PrefillLaunch<BF16, 128>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
+        else PrefillLaunch<BF16, 256>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
     } else {
         if (head_dim == 64) PrefillLaunch<F16, 64>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
-        else PrefillLaunch<F16, 128>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
+        else if (head_dim == 128) PrefillLaunch<F16, 128>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
+        else PrefillLaunch<F16, 256>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
     }
     return check_hip(hipGetLastError(), "prefill_paged launch");
 }
