@@ -198,7 +198,7 @@ size_t ullm_hip_paged_decode_workspace_bytes(int batch, int n_head, int n_kv_hea
  * page_size:   a power of two >= 32; table_stride >= ceil(max_len/page_size)
  * Other arguments as for ullm_hip_attn_decode.  Slots past a sequence's
  * length may hold anything (they are masked and their V rows zeroed).
- * kv_dtype f16 or bf16, head_dim 64, 128 or 256 (else ULLM_HIP_E_UNSUPPORTED). */
+ * kv_dtype f32, f16 or bf16; head_dim 64, 128 or 256 (else ULLM_HIP_E_UNSUPPORTED). */
 int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, const void *v_pages,
                                int kv_dtype, int64_t kv_stride, int page_size, int n_pages,
                                const int32_t *block_table, int table_stride,

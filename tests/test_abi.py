@@ -149,7 +149,7 @@ def test_paged_decode_validation():
         a.update(kw)
         return f(*a.values())
 
-    assert call(dt=L.DT_F32) == L.E_UNSUPPORTED
+    assert call(dt=9) == L.E_UNSUPPORTED
     assert call(d=96) == L.E_UNSUPPORTED
     assert call(page=48) == L.E_INVALID  # not a power of two
     assert call(page=16) == L.E_INVALID  # below one 32-key block

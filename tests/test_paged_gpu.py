@@ -24,7 +24,7 @@ from ullm_amd import _lib as L
 
 pytestmark = pytest.mark.gpu
 
-DT = {"f16": torch.float16, "bf16": torch.bfloat16}
+DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
 
 
 def build(dev, lens, Hk, D, dt, page, pad=0, spare=3, seed=1):
@@ -75,6 +75,8 @@ CASES = [
     ([5000, 4100, 40], 8, 4, 64, "bf16", 32, 37, 0),
     ([33000, 12000], 32, 4, 128, "bf16", 512, 4096, 0),
     ([8192, 3000, 1], 8, 4, 256, "f16", 64, 0, 0),       # head_dim 256 (register-staged kernel)
+    ([512, 40, 1000], 32, 8, 64, "f32", 32, 0, 0),       # the reference's f32 cache (VALU kernel)
+    ([3000, 700], 12, 2, 128, "f32", 64, 333, 4),        # f32 with a binding window
     ([9000, 2000], 16, 8, 256, "bf16", 256, 1024, 16),
 ]
 

@@ -111,6 +111,13 @@ int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64
                 int64_t ss, const int32_t *lens, int max_len, int win, int batch, int nh, int nkv,
                 int D, float qs, float *out, void *ws, size_t ws_bytes, hipStream_t st);
 
+// f32-cache split-KV decode over a paged cache (decode.hip).
+size_t decode_f32_workspace(int batch, int n_head, int n_kv_head, int D, int max_len, int window);
+int decode_f32_paged(const float *q, const void *kp, const void *vp, int64_t kvs,
+                     const int32_t *tab, int tab_stride, int shift, int n_pages,
+                     const int32_t *lens, int max_len, int win, int batch, int nh, int nkv, int D,
+                     float qs, float *out, void *ws, size_t ws_bytes, hipStream_t st);
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 }  // namespace ullm

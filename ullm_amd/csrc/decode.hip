@@ -40,13 +40,22 @@ struct DecodeCfg {
     static_assert(LPT >= 1 && LPT <= 64 && (LPT & (LPT - 1)) == 0, "bad lanes per key");
 };
 
+// Paged K/V for the split-KV kernel (tab == nullptr: contiguous cache).
+// Key t of sequence b is row t % P of page tab[b * stride + t / P]
+// (P = 2^shift); a page index outside the table row or [0, n_pages) reads
+// as zeros.
+struct KeyPages {
+    const int32_t *tab;
+    int stride, shift, n_pages;
+};
+
 template <class T, int D, int G>
 __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
     int n_head, int kv_mul, int n_groups, int chunk, int splits, float qscale,
     float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc,
-    uint32_t *__restrict__ counters) {
+    uint32_t *__restrict__ counters, KeyPages kp) {
     using C = DecodeCfg<T, D, G>;
     constexpr int EPL = C::EPL, LPT = C::LPT, TPW = C::TPW, NW = C::NW, NLG = C::NLG, TT = C::TT;
     constexpr int EB = T::bytes;
@@ -86,20 +95,28 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
     const char *kbase = kc + (int64_t)b * seq_stride * EB + ((int64_t)kvh * D + sub * EPL) * EB;
     const char *vbase = vc + (int64_t)b * seq_stride * EB + ((int64_t)kvh * D + sub * EPL) * EB;
 
+    // Cache row of key t: t itself, or its paged slot (-1: reads zeros).
+    auto key_row = [&](int t) -> int64_t {
+        if (!kp.tab) return t;
+        const int pi = t >> kp.shift;
+        const int phys = pi < kp.stride ? kp.tab[(int64_t)b * kp.stride + pi] : -1;
+        if (phys < 0 || phys >= kp.n_pages) return -1;
+        return ((int64_t)phys << kp.shift) + (t & ((1 << kp.shift) - 1));
+    };
     for (int base = c0; base < c1; base += NLG * TT) {
         u32x4 kr[TT], vr[TT];
         bool ok[TT];
+        int64_t rw[TT];
 #pragma unroll
         for (int i = 0; i < TT; i++) {
             const int t = base + lg + NLG * i;
             ok[i] = t < c1;
-            kr[i] = ok[i] ? ld16_stream(kbase + (int64_t)t * row_bytes) : u32x4{0, 0, 0, 0};
+            rw[i] = ok[i] ? key_row(t) : -1;
+            kr[i] = rw[i] >= 0 ? ld16_stream(kbase + rw[i] * row_bytes) : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
-        for (int i = 0; i < TT; i++) {
-            const int t = base + lg + NLG * i;
-            vr[i] = ok[i] ? ld16_stream(vbase + (int64_t)t * row_bytes) : u32x4{0, 0, 0, 0};
-        }
+        for (int i = 0; i < TT; i++)
+            vr[i] = rw[i] >= 0 ? ld16_stream(vbase + rw[i] * row_bytes) : u32x4{0, 0, 0, 0};
         float s[G][TT];
 #pragma unroll
         for (int i = 0; i < TT; i++) {
@@ -330,24 +347,24 @@ template <class T, int D, int G>
 static void launch_decode(const DecodePlan &p, const float *q, const void *kc, const void *vc,
                           int64_t kv_stride, int64_t seq_stride, const int32_t *lens, int window,
                           int batch, int n_head, int kv_mul, float qscale, float *out, char *ws,
-                          hipStream_t st) {
+                          hipStream_t st, KeyPages kp) {
     dim3 grid(p.splits, p.n_groups, batch);
     hipLaunchKernelGGL((decode_split_kernel<T, D, G>), grid, dim3(kDecodeWaves * 64), 0, st, q,
                        (const char *)kc, (const char *)vc, kv_stride, seq_stride, lens, window,
                        n_head, kv_mul, p.n_groups, p.chunk, p.splits, qscale, out,
-                       (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), (uint32_t *)ws);
+                       (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), (uint32_t *)ws, kp);
 }
 
 template <class T, int D>
 static int dispatch_g(const DecodePlan &p, const float *q, const void *kc, const void *vc,
                       int64_t kvs, int64_t ss, const int32_t *lens, int win, int batch, int nh,
-                      int kv_mul, float qs, float *out, char *ws, hipStream_t st) {
+                      int kv_mul, float qs, float *out, char *ws, hipStream_t st, KeyPages kp) {
     switch (p.G) {
-        case 1: launch_decode<T, D, 1>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st); break;
-        case 2: launch_decode<T, D, 2>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st); break;
-        case 4: launch_decode<T, D, 4>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st); break;
-        case 6: launch_decode<T, D, 6>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st); break;
-        case 8: launch_decode<T, D, 8>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st); break;
+        case 1: launch_decode<T, D, 1>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st, kp); break;
+        case 2: launch_decode<T, D, 2>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st, kp); break;
+        case 4: launch_decode<T, D, 4>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st, kp); break;
+        case 6: launch_decode<T, D, 6>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st, kp); break;
+        case 8: launch_decode<T, D, 8>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st, kp); break;
         default: return set_error(ULLM_HIP_E_UNSUPPORTED, "decode: no kernel for head group %d", p.G);
     }
     return check_hip(hipGetLastError(), "decode launch");
@@ -356,11 +373,12 @@ static int dispatch_g(const DecodePlan &p, const float *q, const void *kc, const
 template <class T>
 static int dispatch_d(int D, const DecodePlan &p, const float *q, const void *kc, const void *vc,
                       int64_t kvs, int64_t ss, const int32_t *lens, int win, int batch, int nh,
-                      int kv_mul, float qs, float *out, char *ws, hipStream_t st) {
+                      int kv_mul, float qs, float *out, char *ws, hipStream_t st,
+                      KeyPages kp = KeyPages{}) {
     switch (D) {
-        case 64: return dispatch_g<T, 64>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st);
-        case 128: return dispatch_g<T, 128>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st);
-        case 256: return dispatch_g<T, 256>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st);
+        case 64: return dispatch_g<T, 64>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st, kp);
+        case 128: return dispatch_g<T, 128>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st, kp);
+        case 256: return dispatch_g<T, 256>(p, q, kc, vc, kvs, ss, lens, win, batch, nh, kv_mul, qs, out, ws, st, kp);
         default: return set_error(ULLM_HIP_E_UNSUPPORTED, "decode: head_dim %d not in {64,128,256}", D);
     }
 }
@@ -423,3 +441,26 @@ extern "C" int ullm_hip_attn_decode(const float *q, const void *k_cache, const v
     return dispatch_d<F32>(head_dim, p, q, k_cache, v_cache, kv_stride, seq_stride, seq_lens,
                            window, batch, n_head, kv_mul, qscale, out, (char *)workspace, st);
 }
+
+namespace ullm {
+
+// f32-cache decode over a paged cache (the paged entry point routes f32
+// here; f16/bf16 go to the MFMA kernels).
+size_t decode_f32_workspace(int batch, int n_head, int n_kv_head, int D, int max_len, int window) {
+    return plan_decode(batch, n_head, n_kv_head, D, ULLM_DT_F32, max_len, window).bytes;
+}
+
+int decode_f32_paged(const float *q, const void *kp, const void *vp, int64_t kvs,
+                     const int32_t *tab, int tab_stride, int shift, int n_pages,
+                     const int32_t *lens, int max_len, int win, int batch, int nh, int nkv, int D,
+                     float qs, float *out, void *ws, size_t ws_bytes, hipStream_t st) {
+    const DecodePlan p = plan_decode(batch, nh, nkv, D, ULLM_DT_F32, max_len, win);
+    if (p.bytes > 0 && (!ws || ws_bytes < p.bytes))
+        return set_error(ULLM_HIP_E_WORKSPACE, "decode_paged: workspace of %zu bytes needed, %zu given",
+                         p.bytes, ws_bytes);
+    return dispatch_d<F32>(D, p, q, kp, vp, kvs, 0, lens, win, batch, nh, nh / nkv, qs, out,
+                           (char *)ws, st, KeyPages{tab, tab_stride, shift, n_pages});
+}
+
+}  // namespace ullm
+

@@ -941,8 +941,10 @@ extern "C" size_t ullm_hip_paged_decode_workspace_bytes(int batch, int n_head, i
                                                         int head_dim, int max_len, int window) {
     if (batch < 1 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || max_len < 1) return 0;
     if (head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
-    return decode_mfma_workspace(batch, n_head, n_kv_head, head_dim, max_len,
-                                 paged_plan_window(window));
+    const size_t m = decode_mfma_workspace(batch, n_head, n_kv_head, head_dim, max_len,
+                                           paged_plan_window(window));
+    const size_t f = decode_f32_workspace(batch, n_head, n_kv_head, head_dim, max_len, window);
+    return m > f ? m : f;
 }
 
 extern "C" int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, const void *v_pages,
@@ -952,22 +954,22 @@ extern "C" int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, c
                                           int window, int batch, int n_head, int n_kv_head,
                                           int head_dim, float scale, float *out, void *workspace,
                                           size_t workspace_bytes, void *stream) {
-    if (kv_dtype != ULLM_DT_F16 && kv_dtype != ULLM_DT_BF16)
-        return set_error(ULLM_HIP_E_UNSUPPORTED, "decode_paged: kv dtype %d (f16/bf16 only)", kv_dtype);
+    if (!dtype_ok(kv_dtype))
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "decode_paged: kv dtype %d", kv_dtype);
     if (head_dim != 64 && head_dim != 128 && head_dim != 256)
         return set_error(ULLM_HIP_E_UNSUPPORTED, "decode_paged: head_dim %d not in {64,128,256}", head_dim);
     if (batch < 1 || batch > 65535 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head)
         return set_error(ULLM_HIP_E_INVALID, "decode_paged: bad heads n_head=%d n_kv_head=%d batch=%d",
                          n_head, n_kv_head, batch);
     if (max_len < 1) return set_error(ULLM_HIP_E_INVALID, "decode_paged: max_len %d < 1", max_len);
-    if (kv_stride < (int64_t)n_kv_head * head_dim || (kv_stride * 2) % 16)
+    if (kv_stride < (int64_t)n_kv_head * head_dim || (kv_stride * dtype_bytes(kv_dtype)) % 16)
         return set_error(ULLM_HIP_E_INVALID,
                          "decode_paged: kv_stride %lld must be >= n_kv_head*head_dim and 16-byte aligned",
                          (long long)kv_stride);
     if (page_size < kTok || (page_size & (page_size - 1)))
         return set_error(ULLM_HIP_E_INVALID, "decode_paged: page_size %d must be a power of two >= %d",
                          page_size, kTok);
-    if ((int64_t)page_size * kv_stride * 2 > 0x7fff0000LL)
+    if ((int64_t)page_size * kv_stride * dtype_bytes(kv_dtype) > 0x7fff0000LL)
         return set_error(ULLM_HIP_E_INVALID, "decode_paged: a page exceeds 2 GiB");
     if (n_pages < 1) return set_error(ULLM_HIP_E_INVALID, "decode_paged: n_pages %d < 1", n_pages);
     if (table_stride < (max_len + page_size - 1) / page_size)
@@ -977,6 +979,11 @@ extern "C" int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, c
         return set_error(ULLM_HIP_E_INVALID, "decode_paged: null tensor pointer");
     if (((uintptr_t)k_pages | (uintptr_t)v_pages | (uintptr_t)q) & 15)
         return set_error(ULLM_HIP_E_INVALID, "decode_paged: q/k_pages/v_pages must be 16-byte aligned");
+    if (kv_dtype == ULLM_DT_F32)
+        return decode_f32_paged(q, k_pages, v_pages, kv_stride, block_table, table_stride,
+                                __builtin_ctz(page_size), n_pages, seq_lens, max_len, window,
+                                batch, n_head, n_kv_head, head_dim, scale * kLog2e, out, workspace,
+                                workspace_bytes, (hipStream_t)stream);
     const MfmaPlan p = plan_mfma(batch, n_head, n_kv_head, head_dim, max_len, paged_plan_window(window));
     if (p.bytes > 0 && (!workspace || workspace_bytes < p.bytes))
         return set_error(ULLM_HIP_E_WORKSPACE, "decode_paged: workspace of %zu bytes needed, %zu given",
