@@ -214,25 +214,33 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
         if (splits == 1) {
             out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
         } else {
-            ws_acc[(unit * splits + split) * (G * D) + idx] = num;
+            // System-coherent stores (written through to memory): the last
+            // workgroup reads them back without an L2 write-back here or an
+            // invalidate there.
+            __hip_atomic_store(ws_acc + (unit * splits + split) * (G * D) + idx, num,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             if (d == 0) {
-                ws_ml[((unit * splits + split) * G + g) * 2 + 0] = mx;
-                ws_ml[((unit * splits + split) * G + g) * 2 + 1] = den;
+                float *ml = ws_ml + ((unit * splits + split) * G + g) * 2;
+                __hip_atomic_store(ml, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(ml + 1, den, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             }
         }
     }
     if (splits == 1) return;
 
-    // Publish the partial; the last workgroup of this unit merges all splits.
-    __threadfence();
+    // Publish the partial (every thread's stores completed, then one relaxed
+    // device-scope count); the last workgroup of this unit merges all splits
+    // with system-coherent loads.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-        const uint32_t prev = atomicAdd(&counters[unit], 1u);
+        const uint32_t prev = __hip_atomic_fetch_add(&counters[unit], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
         sm_last = (prev == (uint32_t)(splits - 1));
     }
     __syncthreads();
     if (!sm_last) return;
-    __threadfence();
+    auto ldc = [](const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
 
     // Merge all splits of this unit.  Loads are issued in parallel: m/l go
     // to LDS first, then thread (column of 4 d, split residue r) walks its
@@ -243,8 +251,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
     float *sl = sw + kMaxSplitsG;                 // [splits*G] partial sums l
     float *sden = sl + kMaxSplitsG;               // [G] denominators
     for (int i = tid; i < splits * G; i += NW * 64) {
-        sw[i] = mlu[2 * i];
-        sl[i] = mlu[2 * i + 1];
+        sw[i] = ldc(mlu + 2 * i);
+        sl[i] = ldc(mlu + 2 * i + 1);
     }
     __syncthreads();
     if (tid < G) {
@@ -269,7 +277,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
         f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
         for (int sp = r; sp < splits; sp += R) {
-            const f32x4 v = *(const f32x4 *)(accu + (int64_t)sp * (G * D) + col * 4);
+            const float *ap = accu + (int64_t)sp * (G * D) + col * 4;
+            const f32x4 v = {ldc(ap), ldc(ap + 1), ldc(ap + 2), ldc(ap + 3)};
             const float w = sw[sp * G + g];
             a[0] += v[0] * w; a[1] += v[1] * w; a[2] += v[2] * w; a[3] += v[3] * w;
         }
@@ -284,7 +293,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
         const float den = sden[g];
         out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
     }
-    if (tid == 0) counters[unit] = 0u;  // leave the counter ready for the next call
+    if (tid == 0)  // leave the counter ready for the next call
+        __hip_atomic_store(&counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
