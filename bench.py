@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "append", "proj", "matmul", "paged", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "append", "proj", "matmul", "paged", "copy", "floor"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     return ap.parse_args()
 
@@ -423,6 +423,52 @@ def bench_copy(torch):
     return dict(bytes_each_way=n)
 
 
+def bench_floor(torch, A):
+    """Read floors beside the decode op: ullm_hip_stream_read over a distinct
+    buffer per graph node (rotated past the MALL), at the cfg2 layer size
+    (4 MiB) and the cfg5 layer size (64 MiB), plus a 16-byte read (the cost
+    of a graph node itself).  Same launch path as the decode op."""
+    import ctypes as C
+
+    lib = A.L.lib()
+    dev = torch.device("cuda")
+    sink = torch.zeros(4096, dtype=torch.int32, device=dev)
+    res = {}
+    for name, nbytes, nodes, grid in (("node", 16, 56, 1), ("read_4MiB", 4 << 20, 140, 1024),
+                                      ("read_64MiB", 64 << 20, 48, 2048)):
+        pool = torch.ones(max(nbytes * nodes // 4, 4), dtype=torch.float32, device=dev)
+        base = pool.data_ptr()
+        step = nbytes if name != "node" else 0
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap):
+            with torch.cuda.graph(g, stream=cap):
+                st = C.c_void_p(cap.cuda_stream)
+                for i in range(nodes):
+                    A.L.check(lib.ullm_hip_stream_read(C.c_void_p(base + i * step), nbytes, grid,
+                                                       C.c_void_p(sink.data_ptr()), st))
+        torch.cuda.current_stream().wait_stream(cap)
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        reps = 20
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            g.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1000.0 / (reps * nodes)
+        res[name + "_us"] = round(us, 3)
+        if name != "node":
+            res[name + "_gbps"] = round(nbytes / (us * 1e3), 1)
+            res[name + "_frac"] = round(nbytes / (us * 1e3) / HBM_PEAK_GBS, 4)
+        del g, pool
+    return res
+
+
 def cpu_baseline_decode(H, Hk, D, L, n_layer, budget_s=12.0):
     """The oracle (single thread, reference schedule) on layers of the same shape."""
     import numpy as np
@@ -485,6 +531,9 @@ def main():
     if args.only == "copy":
         print(json.dumps(bench_copy(torch)))
         return
+    if args.only == "floor":
+        print(json.dumps(bench_floor(torch, A)))
+        return
     res = {}
     if args.only in ("all", "decode"):
         res["cfg2"] = bench_decode(torch, A, args, 12, 2, 128, 4096, 28, torch.float16, "cfg2")
@@ -505,6 +554,8 @@ def main():
         res["cfg5"] = bench_decode(torch, A, argparse.Namespace(steps=max(5, args.steps // 10),
                                                                 warmup=3),
                                    32, 4, 128, 32768, 48, torch.bfloat16, "cfg5")
+    if args.only in ("all",):
+        res["floor"] = bench_floor(torch, A)
     if args.only != "all":
         print(json.dumps(res))
         return
@@ -545,7 +596,9 @@ def main():
                                     "128, bf16 KV 32768, 48 layers",
                         "us_per_layer": round(lc["us_per_layer"], 3),
                         "gbps": round(lc["gbps_step"], 1),
-                        "frac_hbm": round(lc["gbps_step"] / HBM_PEAK_GBS, 4)},
+                        "frac_hbm": round(lc["gbps_step"] / HBM_PEAK_GBS, 4),
+                        "read_floor_us": res["floor"]["read_64MiB_us"],
+                        "read_floor_frac": res["floor"]["read_64MiB_frac"]},
         "append": {"workload": "cfg3 fused append: 2048 rows, 32/8 heads, head_dim 128, f32 "
                                "q/k/v in, Q/K RMSNorm + NeoX RoPE, bf16 q and KV rows out",
                    "kernel": "qkv_append_kernel<128,BF16,BF16>",
@@ -586,7 +639,13 @@ def main():
                      "kernel": "decode_dma_kernel<F16,128,1> + decode_merge_kernel<128,4> "
                                "(one decode-attention op per layer)",
                      "algorithmic_bytes": d["layer_bytes"],
-                     "us_per_launch": round(d["us_per_layer"], 3)},
+                     "us_per_launch": round(d["us_per_layer"], 3),
+                     "read_floor": {
+                         "note": "ullm_hip_stream_read of the same 4 MiB as one graph node: the "
+                                 "best a single read-only launch of this size reaches here",
+                         "us": res["floor"]["read_4MiB_us"],
+                         "frac": res["floor"]["read_4MiB_frac"],
+                         "graph_node_us": res["floor"]["node_us"]}},
         "roofline_prefill": {"bound": "mfma", "achieved": round(p["tflops"], 2),
                              "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(p["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),

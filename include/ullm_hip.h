@@ -241,6 +241,15 @@ int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, const void *
                                 int window, int n_head, int n_kv_head, int head_dim, float scale,
                                 float *out, void *stream);
 
+/* Measurement calibration (no counterpart in the reference): reads `bytes`
+ * bytes of DEVICE memory at `src` (16-byte aligned) once, with 16-byte loads
+ * split over `workgroups` 256-thread workgroups, and writes at most one word
+ * per workgroup into `sink` (DEVICE uint32[workgroups]).  It is the floor a
+ * read-only stream of that size reaches in one launch, against which the
+ * decode op (a read-only stream of its K/V bytes) is compared. */
+int ullm_hip_stream_read(const void *src, size_t bytes, int workgroups, uint32_t *sink,
+                         void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -198,3 +198,14 @@ def test_paged_prefill_validation():
     assert call(hk=3) == L.E_INVALID
     assert call(s=0) == L.OK
     assert call() == L.E_INVALID  # null pointers
+
+
+def test_stream_read_validation():
+    """The calibration read rejects null, unaligned and empty arguments
+    before any HIP call."""
+    lib = L.lib()
+    sink = C.c_void_p(64)
+    assert lib.ullm_hip_stream_read(None, 1024, 4, sink, None) == L.E_INVALID
+    assert lib.ullm_hip_stream_read(C.c_void_p(4096 + 8), 1024, 4, sink, None) == L.E_INVALID
+    assert lib.ullm_hip_stream_read(C.c_void_p(4096), 8, 4, sink, None) == L.E_INVALID
+    assert lib.ullm_hip_stream_read(C.c_void_p(4096), 1024, 0, sink, None) == L.E_INVALID

@@ -27,6 +27,7 @@ SIGNATURES = {
         _i, [_vp, _vp, _vp, _i, _i64, _i, _i, _i, _i, _i, _i, _f, _vp, _vp]
     ),
     "ullm_hip_rope_table": (_i, [_vp, _i, _i, _f]),
+    "ullm_hip_stream_read": (_i, [_vp, _sz, _i, _vp, _vp]),
     "ullm_hip_qkv_append": (
         _i,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _i, _i, _i, _i, _i,

@@ -105,6 +105,10 @@ inline int check_hip(hipError_t e, const char *what) {
 inline int dtype_bytes(int dt) { return dt == ULLM_DT_F32 ? 4 : 2; }
 inline bool dtype_ok(int dt) { return dt == ULLM_DT_F32 || dt == ULLM_DT_F16 || dt == ULLM_DT_BF16; }
 
+// Merge of split-KV partials (decode_mfma.hip): acc [units][splits][gt][D]
+// and (m, l) [units][splits][gt][2] f32, units = batch * n_units.
+void decode_merge_launch(int D, const float *ws_ml, const float *ws_acc, int splits, int gt,
+                         int n_units, int batch, int n_head, float *out, hipStream_t st);
 // MFMA decode path for f16/bf16 caches (decode_mfma.hip).
 size_t decode_mfma_workspace(int batch, int n_head, int n_kv_head, int D, int max_len, int window);
 int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64_t kvs,

@@ -16,9 +16,10 @@
 //    its keys (tiles of TT keys, one max/rescale per tile), so the only
 //    cross-lane traffic in the stream is the LPT-lane dot-product sum (DPP).
 //  * Lane groups merge by shuffles, waves merge through LDS, and chunks
-//    (splits) merge in the same launch: every workgroup publishes its
-//    (m, l, acc) partial, and the last one to arrive for a (b, head group),
-//    found with an agent-scope counter, combines them and writes `out`.
+//    (splits) are combined by decode_merge_kernel (decode_mfma.hip) in a
+//    second launch.  A merge inside this kernel by the last workgroup to
+//    arrive costs more than that launch: one CU then reads every partial of
+//    the unit, after a store-drain and a device-scope counter round trip.
 //  * Softmax runs in the exp2 domain: q is pre-multiplied by scale*log2(e).
 #include "common.hpp"
 #include "wave.hpp"
@@ -54,8 +55,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
     int n_head, int kv_mul, int n_groups, int chunk, int splits, float qscale,
-    float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc,
-    uint32_t *__restrict__ counters, KeyPages kp) {
+    float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc, KeyPages kp) {
     using C = DecodeCfg<T, D, G>;
     constexpr int EPL = C::EPL, LPT = C::LPT, TPW = C::TPW, NW = C::NW, NLG = C::NLG, TT = C::TT;
     constexpr int EB = T::bytes;
@@ -180,13 +180,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
     }
 
     // Merge the waves through LDS.
-    constexpr int kMaxSplitsG = 256;               // splits * G cap (planner)
-    constexpr int R_ = (NW * 64) / (G * D / 4) > 0 ? (NW * 64) / (G * D / 4) : 1;
     constexpr int kAccFloats = NW * G * D;
-    constexpr int kMergeFloats = 2 * kMaxSplitsG + 8 + R_ * G * D;
     __shared__ float sm_ml[NW][G][2];
-    __shared__ __attribute__((aligned(16))) float sm_acc[1][1][kAccFloats > kMergeFloats ? kAccFloats : kMergeFloats];
-    __shared__ int sm_last;
+    __shared__ __attribute__((aligned(16))) float sm_acc[1][1][kAccFloats];
     if (lane < LPT) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -214,87 +210,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
         if (splits == 1) {
             out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
         } else {
-            // System-coherent stores (written through to memory): the last
-            // workgroup reads them back without an L2 write-back here or an
-            // invalidate there.
-            __hip_atomic_store(ws_acc + (unit * splits + split) * (G * D) + idx, num,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            if (d == 0) {
-                float *ml = ws_ml + ((unit * splits + split) * G + g) * 2;
-                __hip_atomic_store(ml, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(ml + 1, den, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            }
+            // The split's partial (O unnormalised, then m, l) for
+            // decode_merge_kernel.
+            ws_acc[(unit * splits + split) * (G * D) + idx] = num;
+            if (d == 0)
+                *(float2 *)(ws_ml + ((unit * splits + split) * G + g) * 2) = float2{mx, den};
         }
     }
-    if (splits == 1) return;
-
-    // Publish the partial (every thread's stores completed, then one relaxed
-    // device-scope count); the last workgroup of this unit merges all splits
-    // with system-coherent loads.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&counters[unit], 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        sm_last = (prev == (uint32_t)(splits - 1));
-    }
-    __syncthreads();
-    if (!sm_last) return;
-    auto ldc = [](const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
-
-    // Merge all splits of this unit.  Loads are issued in parallel: m/l go
-    // to LDS first, then thread (column of 4 d, split residue r) walks its
-    // share of the splits and the R residues are summed through LDS.
-    const float *mlu = ws_ml + unit * splits * G * 2;
-    const float *accu = ws_acc + unit * splits * (G * D);
-    float *sw = &sm_acc[0][0][0];                 // [splits*G] weights, reused LDS
-    float *sl = sw + kMaxSplitsG;                 // [splits*G] partial sums l
-    float *sden = sl + kMaxSplitsG;               // [G] denominators
-    for (int i = tid; i < splits * G; i += NW * 64) {
-        sw[i] = ldc(mlu + 2 * i);
-        sl[i] = ldc(mlu + 2 * i + 1);
-    }
-    __syncthreads();
-    if (tid < G) {
-        float mx = -INFINITY;
-        for (int sp = 0; sp < splits; sp++) mx = fmaxf(mx, sw[sp * G + tid]);
-        sm_ml[0][tid][0] = (mx == -INFINITY) ? 0.f : mx;
-    }
-    __syncthreads();
-    for (int i = tid; i < splits * G; i += NW * 64) sw[i] = exp2f(sw[i] - sm_ml[0][i % G][0]);
-    __syncthreads();
-    if (tid < G) {
-        float den = 0.f;
-        for (int sp = 0; sp < splits; sp++) den += sl[sp * G + tid] * sw[sp * G + tid];
-        sden[tid] = den;
-    }
-    constexpr int NCOL = G * D / 4;
-    constexpr int R = (NW * 64) / NCOL > 0 ? (NW * 64) / NCOL : 1;
-    float *sred = sden + 8;                       // [R][G*D] partial sums
-    if (tid < NCOL * R) {
-        const int col = tid % NCOL, r = tid / NCOL;
-        const int g = (col * 4) / D;
-        f32x4 a = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-        for (int sp = r; sp < splits; sp += R) {
-            const float *ap = accu + (int64_t)sp * (G * D) + col * 4;
-            const f32x4 v = {ldc(ap), ldc(ap + 1), ldc(ap + 2), ldc(ap + 3)};
-            const float w = sw[sp * G + g];
-            a[0] += v[0] * w; a[1] += v[1] * w; a[2] += v[2] * w; a[3] += v[3] * w;
-        }
-        *(f32x4 *)(sred + r * (G * D) + col * 4) = a;
-    }
-    __syncthreads();
-    for (int idx = tid; idx < G * D; idx += NW * 64) {
-        const int g = idx / D, d = idx % D;
-        float num = 0.f;
-#pragma unroll
-        for (int r = 0; r < R; r++) num += sred[r * (G * D) + idx];
-        const float den = sden[g];
-        out[((int64_t)b * n_head + head0 + g) * D + d] = den > 0.f ? num / den : 0.f;
-    }
-    if (tid == 0)  // leave the counter ready for the next call
-        __hip_atomic_store(&counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -316,7 +238,7 @@ static int lanes_per_key(int dtype, int D) { return D / (16 / dtype_bytes(dtype)
 
 // Split-KV plan.  Chunks are multiples of the lane-group count so every lane
 // group gets whole keys; the split count aims at a few workgroups per CU but is
-// capped, because the last workgroup of a unit reads every split's partial.
+// capped at the merge kernel's limit.
 static const int kEnvSplits = env_override("ULLM_HIP_DECODE_SPLITS");
 
 static DecodePlan plan_decode(int batch, int n_head, int n_kv_head, int D, int dtype, int max_len,
@@ -329,11 +251,14 @@ static DecodePlan plan_decode(int batch, int n_head, int n_kv_head, int D, int d
     p.nlg = kDecodeWaves * (64 / lpt);
     const int visible = (window > 0 && max_len > window) ? window : max_len;
     const int units = batch * p.n_groups;
-    // tile = keys one workgroup covers per iteration (every lane group busy).
+    // A context that one workgroup iteration covers (tile keys) is not
+    // split.  Past that, every split holds at least one key per lane group,
+    // so short contexts still spread over about one workgroup per CU
+    // (measured: cfg1-shaped L = 512 over 16 splits 10.6 us per layer, over
+    // 2 splits of one full tile each 12.1 us).
     const int epl = 16 / dtype_bytes(dtype);
-    const int tt = (p.G * epl <= 48) ? 8 : 4;
-    const int tile = p.nlg * tt;
-    int splits = (visible + tile - 1) / tile;             // >= one full tile per split
+    const int tile = p.nlg * ((p.G * epl <= 48) ? 8 : 4);
+    int splits = visible <= tile ? 1 : (visible + p.nlg - 1) / p.nlg;
     const int want = (kTargetWorkgroups + units - 1) / units;
     if (splits > want) splits = want;
     const int merge_cap = 256 / p.G;                       // merge reads <= 256 partial rows
@@ -344,12 +269,11 @@ static DecodePlan plan_decode(int batch, int n_head, int n_kv_head, int D, int d
     chunk = ((chunk + p.nlg - 1) / p.nlg) * p.nlg;
     p.chunk = chunk;
     p.splits = (visible + chunk - 1) / chunk;
-    const size_t ctr = ((size_t)units * 4 + 255) / 256 * 256;
     const size_t ml = ((size_t)units * p.splits * p.G * 2 * 4 + 255) / 256 * 256;
     const size_t ac = (size_t)units * p.splits * p.G * D * 4;
-    p.off_ml = ctr;
-    p.off_acc = ctr + ml;
-    p.bytes = p.splits > 1 ? ctr + ml + ac : 0;
+    p.off_ml = 0;
+    p.off_acc = ml;
+    p.bytes = p.splits > 1 ? ml + ac : 0;
     return p;
 }
 
@@ -362,7 +286,10 @@ static void launch_decode(const DecodePlan &p, const float *q, const void *kc, c
     hipLaunchKernelGGL((decode_split_kernel<T, D, G>), grid, dim3(kDecodeWaves * 64), 0, st, q,
                        (const char *)kc, (const char *)vc, kv_stride, seq_stride, lens, window,
                        n_head, kv_mul, p.n_groups, p.chunk, p.splits, qscale, out,
-                       (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), (uint32_t *)ws, kp);
+                       (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), kp);
+    if (p.splits > 1)
+        decode_merge_launch(D, (const float *)(ws + p.off_ml), (const float *)(ws + p.off_acc),
+                            p.splits, G, p.n_groups, batch, n_head, out, st);
 }
 
 template <class T, int D>

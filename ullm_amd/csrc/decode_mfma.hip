@@ -850,6 +850,20 @@ static void launch_merge(const MfmaPlan &p, int batch, int nh, float *out, char 
 #undef ULLM_MERGE
 }
 
+void decode_merge_launch(int D, const float *ws_ml, const float *ws_acc, int splits, int gt,
+                         int n_units, int batch, int n_head, float *out, hipStream_t st) {
+    MfmaPlan p{};
+    p.splits = splits;
+    p.gt = gt;
+    p.n_units = n_units;
+    p.off_ml = 0;
+    p.off_acc = (size_t)((const char *)ws_acc - (const char *)ws_ml);
+    char *ws = (char *)ws_ml;
+    if (D == 64) launch_merge<64>(p, batch, n_head, out, ws, st);
+    else if (D == 128) launch_merge<128>(p, batch, n_head, out, ws, st);
+    else launch_merge<256>(p, batch, n_head, out, ws, st);
+}
+
 template <class T, int D>
 static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const void *vc,
                         int64_t kvs, int64_t ss, const int32_t *lens, int max_len, int win,
