@@ -53,10 +53,8 @@ const char *ullm_hip_last_error(void);
 /* Bytes of device workspace ullm_hip_attn_decode needs for this shape.
  * max_len is the largest seq_len the calls will see; a workspace sized for
  * max_len serves every call whose own max_len is smaller.  The workspace holds
- * split-KV partials plus a counter area that must be ZERO before its first
- * use; every completed decode call leaves the counters at zero again, so
- * one hipMemset at allocation suffices.  One workspace serves one stream at
- * a time. */
+ * the split-KV partials; every call writes before it reads, so it needs no
+ * initialisation.  One workspace serves one stream at a time. */
 size_t ullm_hip_decode_workspace_bytes(int batch, int n_head, int n_kv_head, int head_dim,
                                        int max_len, int window);
 
@@ -175,8 +173,8 @@ size_t ullm_hip_qkv_proj_workspace_bytes(int rows, int n_head, int n_kv_head, in
 int ullm_hip_matmul(const void *w, int w_dtype, const float *x, float *y, int in_dim,
                     int out_dim, int n_cols, void *stream);
 
-/* Bytes of workspace ullm_hip_attn_decode_paged needs (same meaning and
- * zero-once rule as ullm_hip_decode_workspace_bytes). */
+/* Bytes of workspace ullm_hip_attn_decode_paged needs (same meaning as
+ * ullm_hip_decode_workspace_bytes). */
 size_t ullm_hip_paged_decode_workspace_bytes(int batch, int n_head, int n_kv_head, int head_dim,
                                              int max_len, int window);
 

@@ -47,7 +47,8 @@ def decode_workspace_bytes(batch, n_head, n_kv_head, head_dim, max_len, window=0
 
 
 def new_decode_workspace(batch, n_head, n_kv_head, head_dim, max_len, window=0, device="cuda"):
-    """Zeroed workspace for attn_decode (the counter area must start at zero)."""
+    """Workspace for attn_decode (split partials; zeroed only for determinism of
+    unused bytes, the kernels write every partial before reading it)."""
     n = max(decode_workspace_bytes(batch, n_head, n_kv_head, head_dim, max_len, window), 256)
     return torch.zeros(n, dtype=torch.uint8, device=device)
 
