@@ -780,8 +780,13 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     const int tile = p.mw * kTok;
     int splits = (visible + tile - 1) / tile;
     const int want = (kMfmaTargetWG * (p.mw == kMW ? 1 : 2) + units - 1) / units;
-    if (blocks <= kMW * 4) splits = 1;
     if (splits > want) splits = want;
+    // head_dim 256 (4-wave workgroups): a short context would leave most CUs
+    // idle at one tile per split, so splits go down to one 32-key block
+    // (the waves past the split's keys contribute nothing).  Measured at
+    // cfg4's 1024-key window: 32 splits per kv head 9.3 us, 8 splits 11.6 us.
+    if (D > 128 && splits < want) splits = std::min(want, blocks);
+    if (blocks <= kMW * 4) splits = 1;
     const int cap = kMaxSplits;
     if (splits > cap) splits = cap;
     if (kEnvSplitsM >= 1) splits = kEnvSplitsM < cap ? kEnvSplitsM : cap;  // tuning override
