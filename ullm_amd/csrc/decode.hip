@@ -50,14 +50,18 @@ struct KeyPages {
     int stride, shift, n_pages;
 };
 
-template <class T, int D, int G>
+// TTK: keys per lane group per tile when the split is shorter than a full
+// tile (1 or 2; 0 = the configuration's TT), so short splits do not compute
+// masked key slots.
+template <class T, int D, int G, int TTK = 0>
 __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
     int n_head, int kv_mul, int n_groups, int chunk, int splits, float qscale,
     float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc, KeyPages kp) {
     using C = DecodeCfg<T, D, G>;
-    constexpr int EPL = C::EPL, LPT = C::LPT, TPW = C::TPW, NW = C::NW, NLG = C::NLG, TT = C::TT;
+    constexpr int EPL = C::EPL, LPT = C::LPT, TPW = C::TPW, NW = C::NW, NLG = C::NLG;
+    constexpr int TT = TTK > 0 && TTK < C::TT ? TTK : C::TT;
     constexpr int EB = T::bytes;
 
     const int split = blockIdx.x, grp = blockIdx.y, b = blockIdx.z;
@@ -283,10 +287,16 @@ static void launch_decode(const DecodePlan &p, const float *q, const void *kc, c
                           int batch, int n_head, int kv_mul, float qscale, float *out, char *ws,
                           hipStream_t st, KeyPages kp) {
     dim3 grid(p.splits, p.n_groups, batch);
-    hipLaunchKernelGGL((decode_split_kernel<T, D, G>), grid, dim3(kDecodeWaves * 64), 0, st, q,
-                       (const char *)kc, (const char *)vc, kv_stride, seq_stride, lens, window,
-                       n_head, kv_mul, p.n_groups, p.chunk, p.splits, qscale, out,
-                       (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), kp);
+    const int kpl = (p.chunk + p.nlg - 1) / p.nlg;  // keys per lane group
+#define ULLM_SPLIT(TTK)                                                                        \
+    hipLaunchKernelGGL((decode_split_kernel<T, D, G, TTK>), grid, dim3(kDecodeWaves * 64), 0, st, \
+                       q, (const char *)kc, (const char *)vc, kv_stride, seq_stride, lens,      \
+                       window, n_head, kv_mul, p.n_groups, p.chunk, p.splits, qscale, out,      \
+                       (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), kp)
+    if (kpl <= 1) ULLM_SPLIT(1);
+    else if (kpl <= 2) ULLM_SPLIT(2);
+    else ULLM_SPLIT(0);
+#undef ULLM_SPLIT
     if (p.splits > 1)
         decode_merge_launch(D, (const float *)(ws + p.off_ml), (const float *)(ws + p.off_acc),
                             p.splits, G, p.n_groups, batch, n_head, out, st);
