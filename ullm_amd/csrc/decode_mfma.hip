@@ -673,12 +673,13 @@ constexpr int kMaxSplits = 256;
 
 // Combines the split partials of one (sequence, head) in one round trip.
 // A workgroup takes D/4/kMergeGroups four-column groups of one head (the
-// merge of a few heads then still spreads over many CUs); every load (the
-// split rows of this thread's column group, then this thread's split m/l) is
-// issued branch-free (indices clamped, weights of clamped duplicates zeroed)
-// before any is consumed; then the log-sum-exp weights are applied and the R
-// split residues summed through LDS.  NL = partial rows per thread,
-// ceil(splits / R).
+// merge of a few heads then still spreads over many CUs).  Every load is
+// issued branch-free before any is consumed: the split rows of this thread's
+// column group with their m (indices clamped, weights of clamped duplicates
+// zeroed), and the (m, l) of splits lane, lane + 64, ... from which every
+// wave forms the maximum and the denominator by itself.  The only LDS round
+// trip is the final sum of the R split residues across the waves.
+// NL = partial rows per thread, ceil(splits / R).
 constexpr int kMergeThreads = 256;
 constexpr int kMergeGroups = 4;
 template <int D, int NL>
@@ -686,39 +687,41 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     const float *__restrict__ ws_ml, const float *__restrict__ ws_acc, int splits, int gt,
     int n_units, int n_head, float *__restrict__ out) {
     constexpr int NC = D / 4 / kMergeGroups, R = kMergeThreads / NC;
+    constexpr int NML = kMaxSplits / 64;  // (m, l) pairs per lane
     const int g = blockIdx.x / kMergeGroups, cg = blockIdx.x % kMergeGroups;
     const int unit = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, col = tid % NC, r = tid / NC, lane = tid & 63;
     const int64_t u = (int64_t)b * n_units + unit;
     const int GD = gt * D;
-    __shared__ float sm_m[kMaxSplits], sm_l[kMaxSplits], sm_w[kMaxSplits];
     __shared__ f32x4 red[kMergeThreads / 64][NC];
     const int c4 = cg * NC + col;  // four-column group within the head
     const float *accp = ws_acc + u * splits * GD + g * D + c4 * 4;
+    const float2 *mlu = (const float2 *)ws_ml + u * splits * gt + g;  // split sp at [sp * gt]
     f32x4 v[NL];
+    float mt[NL];
 #pragma unroll
-    for (int i = 0; i < NL; i++)
-        v[i] = *(const f32x4 *)(accp + (int64_t)min(r + i * R, splits - 1) * GD);
-    for (int sp = tid; sp < splits; sp += kMergeThreads) {
-        const float2 ml = *(const float2 *)(ws_ml + ((u * splits + sp) * gt + g) * 2);
-        sm_m[sp] = ml.x;
-        sm_l[sp] = ml.y;
+    for (int i = 0; i < NL; i++) {
+        const int sp = min(r + i * R, splits - 1);
+        v[i] = *(const f32x4 *)(accp + (int64_t)sp * GD);
+        mt[i] = mlu[(int64_t)sp * gt].x;
     }
-    __syncthreads();
-    // max over splits, one redundant reduction per wave
+    float2 ml[NML];
+#pragma unroll
+    for (int j = 0; j < NML; j++) {
+        const int sp = lane + 64 * j;
+        ml[j] = mlu[(int64_t)min(sp, splits - 1) * gt];
+        if (sp >= splits) ml[j] = float2{-INFINITY, 0.f};
+    }
     float mx = -INFINITY;
-    for (int sp = lane; sp < splits; sp += 64) mx = fmaxf(mx, sm_m[sp]);
+#pragma unroll
+    for (int j = 0; j < NML; j++) mx = fmaxf(mx, ml[j].x);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     const float mu = mx == -INFINITY ? 0.f : mx;
-    for (int sp = tid; sp < splits; sp += kMergeThreads)
-        sm_w[sp] = __builtin_amdgcn_exp2f(sm_m[sp] - mu);
-    __syncthreads();
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NL; i++) {
-        const int sp = r + i * R;
-        const float w = sp < splits ? sm_w[sp] : 0.f;
+        const float w = r + i * R < splits ? __builtin_amdgcn_exp2f(mt[i] - mu) : 0.f;
         a += v[i] * w;
     }
     // Sum the split residues: across the lanes of a wave holding one column
@@ -731,7 +734,8 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     __syncthreads();
     if (tid < 64) {  // wave 0: the denominator, then the NC output columns
         float den = 0.f;
-        for (int sp = lane; sp < splits; sp += 64) den += sm_l[sp] * sm_w[sp];
+#pragma unroll
+        for (int j = 0; j < NML; j++) den += ml[j].y * __builtin_amdgcn_exp2f(ml[j].x - mu);
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o, 64);
         const float inv = den > 0.f ? 1.0f / den : 0.f;
