@@ -209,3 +209,41 @@ def test_stream_read_validation():
     assert lib.ullm_hip_stream_read(C.c_void_p(4096 + 8), 1024, 4, sink, None) == L.E_INVALID
     assert lib.ullm_hip_stream_read(C.c_void_p(4096), 8, 4, sink, None) == L.E_INVALID
     assert lib.ullm_hip_stream_read(C.c_void_p(4096), 1024, 0, sink, None) == L.E_INVALID
+
+
+def _needed_ws(dt, h, hk, d, n, win, paged=False):
+    """Workspace bytes one decode call of max_len n asks for, read from the
+    E_WORKSPACE message (the call stops there, before any device work; a
+    call that needs none gets as far as the launch and fails without a GPU)."""
+    lib = L.lib()
+    fake = C.c_void_p(0x10000)
+    kvs = hk * d
+    if paged:
+        rc = lib.ullm_hip_attn_decode_paged(fake, fake, fake, dt, kvs, 32, 1 << 20, fake,
+                                            (n + 31) // 32, fake, n, win, 1, h, hk, d, 0.1,
+                                            fake, None, 0, None)
+    else:
+        rc = lib.ullm_hip_attn_decode(fake, fake, fake, dt, kvs, 0, fake, n, win, 1, h, hk, d,
+                                      0.1, fake, None, 0, None)
+    if rc == L.E_WORKSPACE:
+        m = re.search(rb"workspace of (\d+) bytes needed", lib.ullm_hip_last_error())
+        return int(m.group(1))
+    assert rc in (L.OK, L.E_HIP), (rc, lib.ullm_hip_last_error())
+    return 0
+
+
+@pytest.mark.parametrize("dt", [L.DT_F32, L.DT_F16, L.DT_BF16])
+@pytest.mark.parametrize("shape", [(12, 2, 128), (32, 8, 64), (8, 4, 256)])
+@pytest.mark.parametrize("n_ctx,win", [(1024, 0), (700, 0), (1024, 300), (2048, 1000)])
+@pytest.mark.parametrize("paged", [False, True])
+def test_workspace_for_n_ctx_bounds_every_shorter_call(dt, shape, n_ctx, win, paged):
+    """A workspace sized for max_len = n_ctx serves every call with a smaller
+    max_len (the header's promise), for every cache dtype, including the f32
+    path whose split count is not monotonic in the length."""
+    h, hk, d = shape
+    fn = (L.lib().ullm_hip_paged_decode_workspace_bytes if paged
+          else L.lib().ullm_hip_decode_workspace_bytes)
+    bound = fn(1, h, hk, d, n_ctx, win)
+    for n in range(1, n_ctx + 1):
+        need = _needed_ws(dt, h, hk, d, n, win, paged)
+        assert need <= bound, f"max_len {n}: needs {need} > {bound} sized for {n_ctx}"

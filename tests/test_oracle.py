@@ -229,6 +229,42 @@ def test_qkv_append_composition():
     np.testing.assert_array_equal(qo2[0, :D], ora.rope(h0, 1, D, D, sp, 1e4, False))
 
 
+def test_qkv_append_bias_closed_form():
+    """Bias terms (lib.rs:1021-1034): with norm off and pos 0 (RoPE is the
+    identity there), q_out = q + b_q, K = k + b_k and V = v + b_v bit for bit
+    (one f32 add each).  At pos > 0 the bias goes in before the rotation:
+    the biased append equals the unbiased append of (q + b_q, k + b_k,
+    v + b_v); a bias added after RoPE, or only to some rows or heads, or the
+    wrong bias vector on a tensor, fails one of the two checks."""
+    H, Hk, D, rows = 4, 2, 64, 3
+    q = RNG.standard_normal((rows, H * D)).astype(np.float32)
+    k = RNG.standard_normal((rows, Hk * D)).astype(np.float32)
+    v = RNG.standard_normal((rows, Hk * D)).astype(np.float32)
+    qb = RNG.standard_normal(H * D).astype(np.float32)
+    kb = RNG.standard_normal(Hk * D).astype(np.float32)
+    vb = RNG.standard_normal(Hk * D).astype(np.float32)
+    for neox in (True, False):
+        kc = np.zeros((rows, Hk * D), np.float32)
+        vc = np.zeros_like(kc)
+        qo = ora.qkv_append(q[:1].copy(), k[:1].copy(), v[:1].copy(), 0, H, Hk, D, D, 1e6, neox,
+                            kc, vc, q_bias=qb, k_bias=kb, v_bias=vb)
+        np.testing.assert_array_equal(qo[0], q[0] + qb)
+        np.testing.assert_array_equal(kc[0], k[0] + kb)
+        np.testing.assert_array_equal(vc[0], v[0] + vb)
+        sp = 7
+        kc1 = np.zeros((sp + rows, Hk * D), np.float32)
+        vc1 = np.zeros_like(kc1)
+        kc2, vc2 = kc1.copy(), vc1.copy()
+        qo1 = ora.qkv_append(q, k, v, sp, H, Hk, D, D, 1e6, neox, kc1, vc1, q_bias=qb,
+                             k_bias=kb, v_bias=vb)
+        qo2 = ora.qkv_append(q + qb, k + kb, v + vb, sp, H, Hk, D, D, 1e6, neox, kc2, vc2)
+        np.testing.assert_array_equal(qo1, qo2)
+        np.testing.assert_array_equal(kc1, kc2)
+        np.testing.assert_array_equal(vc1, vc2)
+        assert not np.array_equal(qo1, ora.qkv_append(q, k, v, sp, H, Hk, D, D, 1e6, neox,
+                                                      kc2.copy(), vc2.copy()) + qb)
+
+
 def test_split_kv_merge_math():
     """The (m, l, acc) log-sum-exp merge the GPU kernels use equals one softmax."""
     L, D = 200, 16

@@ -99,3 +99,51 @@ def test_rejects_f32(dev):
     with pytest.raises(A.L.UllmHipError) as e:
         A.attn_prefill(q, q, q, 1, 1, 128)
     assert e.value.code == A.L.E_UNSUPPORTED
+
+
+def test_cfg3_pipeline_norm_rope_all_rows(dev):
+    """cfg3 as BASELINE configures it, end to end at full size: raw f32 Q/K/V
+    ~ N(0,1) -> fused append (per-head RMSNorm with unit weights, eps 1e-6,
+    NeoX RoPE theta 1e6, bf16 q and cache) -> causal prefill, every one of the
+    2048 rows of all 32 heads against the oracle (lib.rs:1035-1058 then
+    :1061-1087).
+
+    Two comparisons:
+     * the prefill kernel against the oracle's prefill on the very bf16
+       values the GPU append produced (same inputs, the attention tolerance);
+     * the whole GPU pipeline against the oracle's pipeline, whose prepared
+       q/K/V are rounded to bf16 the same way (the RMS sums differ in order,
+       so single values may round one bf16 ulp apart; held to the same
+       tolerance)."""
+    S, H, Hk, D, theta = 2048, 32, 8, 128, 1e6
+    print(f"[prefill] cfg3 pipeline S{S} H{H} Hk{Hk} D{D}", flush=True)
+    q = synth.randn(31, 1, (S, H * D))
+    k = synth.randn(31, 2, (S, Hk * D))
+    v = synth.randn(31, 3, (S, Hk * D))
+    ones = torch.ones(D)
+    cs = A.rope_table(S, D, theta, device=dev)
+    kc = torch.zeros(S, Hk * D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    qb = A.qkv_append(q.to(dev), k.to(dev), v.to(dev), kc, vc, cs, start_pos=0, n_head=H,
+                      n_kv_head=Hk, head_dim=D, rotary_dim=D, neox=True, q_norm=ones.to(dev),
+                      k_norm=ones.to(dev), eps=1e-6, q_dtype=torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+    out = A.attn_prefill(qb, kc, vc, H, Hk, D, scale=scale)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    gq, gk, gv = (t.float().cpu().numpy() for t in (qb, kc, vc))
+    ref = ora.attn_prefill(gq, gk, gv, S, 0, H, Hk, D, scale)
+    assert_close(out, ref, what="cfg3 prefill on the GPU-prepared inputs")
+
+    okc = np.zeros((S, Hk * D), np.float32)
+    ovc = np.zeros_like(okc)
+    on = ones.numpy().copy()
+    oq = ora.qkv_append(q.numpy().copy(), k.numpy().copy(), v.numpy().copy(), 0, H, Hk, D, D,
+                        theta, True, okc, ovc, q_norm=on, k_norm=on, eps=1e-6)
+    r16 = lambda x: torch.from_numpy(x).to(torch.bfloat16).float().numpy()  # noqa: E731
+    oq, okc, ovc = r16(oq), r16(okc), r16(ovc)
+    for name, got, want in (("q", gq, oq), ("k", gk, okc), ("v", gv, ovc)):
+        ulp = np.abs(got - want) / np.maximum(np.abs(want), 2.0**-126)
+        assert ulp.max() <= 2.0**-7, f"append {name}: {ulp.max():.3e} > one bf16 ulp"
+    ref2 = ora.attn_prefill(oq, okc, ovc, S, 0, H, Hk, D, scale)
+    assert_close(out, ref2, what="cfg3 pipeline vs the oracle pipeline")

@@ -24,6 +24,7 @@
 #include "common.hpp"
 #include "wave.hpp"
 #include <cstdlib>
+#include <algorithm>
 
 namespace ullm {
 
@@ -355,7 +356,8 @@ extern "C" size_t ullm_hip_decode_workspace_bytes(int batch, int n_head, int n_k
     if (batch < 1 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || max_len < 1) return 0;
     // The f32 cache has the most lanes per key and thus the smallest chunks:
     // size for the largest plan over the three dtypes.
-    size_t best = plan_decode(batch, n_head, n_kv_head, head_dim, ULLM_DT_F32, max_len, window).bytes;
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
+    size_t best = decode_f32_workspace(batch, n_head, n_kv_head, head_dim, max_len, window);
     const size_t m = decode_mfma_workspace(batch, n_head, n_kv_head, head_dim, max_len, window);
     return m > best ? m : best;
 }
@@ -393,8 +395,27 @@ namespace ullm {
 
 // f32-cache decode over a paged cache (the paged entry point routes f32
 // here; f16/bf16 go to the MFMA kernels).
+// Upper bound over every call whose max_len' <= max_len.  plan_decode's
+// split count is not monotonic in the length (its chunks round up to whole
+// lane groups, so a longer context can plan fewer splits), but it never
+// exceeds min(want, merge cap, ceil(visible / nlg)), and each of those grows
+// with the length: size for that many splits.
 size_t decode_f32_workspace(int batch, int n_head, int n_kv_head, int D, int max_len, int window) {
-    return plan_decode(batch, n_head, n_kv_head, D, ULLM_DT_F32, max_len, window).bytes;
+    const DecodePlan p = plan_decode(batch, n_head, n_kv_head, D, ULLM_DT_F32, max_len, window);
+    const int visible = (window > 0 && max_len > window) ? window : max_len;
+    const int epl = 16 / dtype_bytes(ULLM_DT_F32);
+    const int tile = p.nlg * ((p.G * epl <= 48) ? 8 : 4);
+    if (visible <= tile) return 0;  // every shorter call runs unsplit too
+    const int units = batch * p.n_groups;
+    const int want = (kTargetWorkgroups + units - 1) / units;
+    const int merge_cap = 256 / p.G;
+    int smax = (visible + p.nlg - 1) / p.nlg;
+    if (smax > want) smax = want;
+    if (smax > merge_cap) smax = merge_cap;
+    if (kEnvSplits >= 1) smax = std::max(smax, std::min(kEnvSplits, merge_cap));
+    if (smax <= 1) return 0;
+    const size_t ml = ((size_t)units * smax * p.G * 2 * 4 + 255) / 256 * 256;
+    return ml + (size_t)units * smax * p.G * D * 4;
 }
 
 int decode_f32_paged(const float *q, const void *kp, const void *vp, int64_t kvs,
