@@ -113,8 +113,8 @@ def test_cfg3_pipeline_norm_rope_all_rows(dev):
        values the GPU append produced (same inputs, the attention tolerance);
      * the whole GPU pipeline against the oracle's pipeline, whose prepared
        q/K/V are rounded to bf16 the same way (the RMS sums differ in order,
-       so single values may round one bf16 ulp apart; held to the same
-       tolerance)."""
+       so single values may round one bf16 ulp apart, and fewer than 1 %
+       may differ at all; held to the same tolerance)."""
     S, H, Hk, D, theta = 2048, 32, 8, 128, 1e6
     print(f"[prefill] cfg3 pipeline S{S} H{H} Hk{Hk} D{D}", flush=True)
     q = synth.randn(31, 1, (S, H * D))
@@ -142,8 +142,12 @@ def test_cfg3_pipeline_norm_rope_all_rows(dev):
                         theta, True, okc, ovc, q_norm=on, k_norm=on, eps=1e-6)
     r16 = lambda x: torch.from_numpy(x).to(torch.bfloat16).float().numpy()  # noqa: E731
     oq, okc, ovc = r16(oq), r16(okc), r16(ovc)
+    # One bf16 ulp of a value in [1, 2) is 2^-7; below 1 the bound is absolute
+    # (RoPE's a*cos - b*sin can cancel, so a one-ulp difference in the normed
+    # input is no longer one ulp of a small output).
     for name, got, want in (("q", gq, oq), ("k", gk, okc), ("v", gv, ovc)):
-        ulp = np.abs(got - want) / np.maximum(np.abs(want), 2.0**-126)
-        assert ulp.max() <= 2.0**-7, f"append {name}: {ulp.max():.3e} > one bf16 ulp"
+        d = np.abs(got - want) / np.maximum(np.abs(want), 1.0)
+        assert d.max() <= 2.0**-7, f"append {name}: {d.max():.3e} > one bf16 ulp"
+        assert np.mean(got != want) < 0.01, f"append {name}: {np.mean(got != want):.3%} differ"
     ref2 = ora.attn_prefill(oq, okc, ovc, S, 0, H, Hk, D, scale)
     assert_close(out, ref2, what="cfg3 pipeline vs the oracle pipeline")

@@ -516,8 +516,12 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
     for (int i = 0; i < NDT; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_part = 0.f;
 
-    auto consume = [&](const char *kt, int tb) {
+    // more: the other stage is in flight behind this one.  The K tile is
+    // waited for first and V stays in flight through Q.K and the softmax.
+    auto consume = [&](const char *kt, int tb, bool more) {
         const char *vt = kt + TILE;
+        if (more) __builtin_amdgcn_s_waitcnt(vm_wait(3 * NI));
+        else __builtin_amdgcn_s_waitcnt(vm_wait(NI));
         // S^T = K . Q^T: lane (key t*16 + n16, chunk s*4 + kg)
         const uint32_t kbase = lds_addr(kt);
         u32x4 ka[2 * NS];
@@ -585,6 +589,8 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
                 ph[j] = pack2<T>(p[2 * j], p[2 * j + 1]);
             }
         }
+        if (more) __builtin_amdgcn_s_waitcnt(vm_wait(2 * NI));
+        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
         if ((fetch_len > 0 || PG) && tb + kTok > c1) {
             // Fetched rows at or past the length hold whatever the cache
             // holds there (P is 0 for them, but 0 * NaN is NaN): zero them.
@@ -627,15 +633,11 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
     // from there on "issued" is "below c1".
     for (int tb = tb0; tb < c1; tb += 2 * STEP) {
         const bool next1 = tb == tb0 ? tb + STEP < cf : tb + STEP < c1;
-        if (next1) __builtin_amdgcn_s_waitcnt(vm_wait(2 * NI));  // stage 1 in flight
-        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
-        consume(wb0, tb);
+        consume(wb0, tb, next1);  // stage 1 in flight behind it when next1
         __builtin_amdgcn_s_waitcnt(kLgkm0);
         if (tb + 2 * STEP < c1) issue(wb0, tb + 2 * STEP);
         if (tb + STEP >= c1) break;
-        if (tb + 2 * STEP < c1) __builtin_amdgcn_s_waitcnt(vm_wait(2 * NI));
-        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
-        consume(wb1, tb + STEP);
+        consume(wb1, tb + STEP, tb + 2 * STEP < c1);
         __builtin_amdgcn_s_waitcnt(kLgkm0);
         if (tb + 3 * STEP < c1) issue(wb1, tb + 3 * STEP);
     }
@@ -682,12 +684,13 @@ constexpr int kMaxSplits = 256;
 // NL = partial rows per thread, ceil(splits / R).
 constexpr int kMergeThreads = 256;
 constexpr int kMergeGroups = 4;
-template <int D, int NL>
+// NML = (m, l) pairs per lane, ceil(splits / 64).
+template <int D, int NL, int NML>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     const float *__restrict__ ws_ml, const float *__restrict__ ws_acc, int splits, int gt,
     int n_units, int n_head, float *__restrict__ out) {
     constexpr int NC = D / 4 / kMergeGroups, R = kMergeThreads / NC;
-    constexpr int NML = kMaxSplits / 64;  // (m, l) pairs per lane
+    static_assert(NML * 64 <= kMaxSplits, "merge reads at most kMaxSplits (m, l) pairs");
     const int g = blockIdx.x / kMergeGroups, cg = blockIdx.x % kMergeGroups;
     const int unit = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, col = tid % NC, r = tid / NC, lane = tid & 63;
@@ -849,14 +852,25 @@ static void launch_merge(const MfmaPlan &p, int batch, int nh, float *out, char 
     const int nl = (p.splits + R - 1) / R;
     const dim3 g(p.gt * kMergeGroups, p.n_units, batch);
     const float *ml = (const float *)(ws + p.off_ml), *ac = (const float *)(ws + p.off_acc);
-#define ULLM_MERGE(NL) hipLaunchKernelGGL((decode_merge_kernel<D, NL>), g, dim3(kMergeThreads), 0, \
-                                          st, ml, ac, p.splits, p.gt, p.n_units, nh, out)
-    if (nl <= 1) ULLM_MERGE(1);
-    else if (nl <= 2) ULLM_MERGE(2);
-    else if (nl <= 4) ULLM_MERGE(4);
-    else if (nl <= 8) ULLM_MERGE(8);
-    else ULLM_MERGE(16);
-#undef ULLM_MERGE
+    // (m, l) loads per lane: as many as the splits need, not kMaxSplits / 64.
+    auto go = [&](auto nlc) {
+        constexpr int NL = decltype(nlc)::value;
+        if (p.splits <= 64)
+            hipLaunchKernelGGL((decode_merge_kernel<D, NL, 1>), g, dim3(kMergeThreads), 0, st, ml,
+                               ac, p.splits, p.gt, p.n_units, nh, out);
+        else if (p.splits <= 128)
+            hipLaunchKernelGGL((decode_merge_kernel<D, NL, 2>), g, dim3(kMergeThreads), 0, st, ml,
+                               ac, p.splits, p.gt, p.n_units, nh, out);
+        else
+            hipLaunchKernelGGL((decode_merge_kernel<D, NL, kMaxSplits / 64>), g,
+                               dim3(kMergeThreads), 0, st, ml, ac, p.splits, p.gt, p.n_units, nh,
+                               out);
+    };
+    if (nl <= 1) go(Int<1>{});
+    else if (nl <= 2) go(Int<2>{});
+    else if (nl <= 4) go(Int<4>{});
+    else if (nl <= 8) go(Int<8>{});
+    else go(Int<16>{});
 }
 
 void decode_merge_launch(int D, const float *ws_ml, const float *ws_acc, int splits, int gt,
