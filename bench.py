@@ -7,10 +7,13 @@ of 4096 positions, 28 layers back to back.  One step = the attention of all
 over >= 512 MiB so the 256 MiB Infinity Cache cannot serve them.
 
 Also reported on the same line: causal prefill (configs[2], Qwen3-4B-shaped,
-S=2048 bf16) in TFLOP/s, long-context decode (configs[4], 32K bf16), the
-roofline of the dominant kernel and the CPU oracle on a bounded sample.
+S=2048 bf16) in TFLOP/s, the cfg1 (f32, configs[0]) and cfg4 (Gemma-3 head_dim
+256: a 6-layer sliding-window/global decode group and its S=1024 prefill)
+rows, long-context decode (configs[4], 32K bf16), the roofline of the
+dominant kernel, the CPU oracle on a bounded sample, and the GPU outputs of
+the SplitMix64 inputs against the oracle's.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|long|append|proj|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only PART] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -35,16 +38,25 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "append", "proj", "matmul", "paged", "copy", "floor"], default="all")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "append", "proj",
+                                       "matmul", "paged", "cfg1", "cfg4", "copy", "floor"],
+                    default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     return ap.parse_args()
 
 
-def decode_workload(torch, A, H, Hk, D, L, n_layer, dt, min_bytes):
-    """Rotating sets of per-layer (q, K, V) plus one captured graph per set."""
+def decode_workload(torch, A, H, Hk, D, L, n_layer, dt, min_bytes, windows=None, first=None):
+    """Rotating sets of per-layer (q, K, V) plus one captured graph per set.
+    windows[l]: the sliding window of layer l (0: global).  first: (q, K, V)
+    CPU tensors for layer 0 of set 0 (the SplitMix64 layer the CPU baseline
+    runs too); every other layer is torch-random."""
     dev = torch.device("cuda")
-    layer_bytes = 2 * L * Hk * D * torch.finfo(dt).bits // 8
-    n_sets = max(1, math.ceil(min_bytes / (layer_bytes * n_layer)))
+    windows = windows or [0] * n_layer
+    esz = torch.finfo(dt).bits // 8
+    visible = [min(L, w) if w > 0 else L for w in windows]
+    layer_bytes = [2 * n * Hk * D * esz for n in visible]
+    alloc = 2 * L * Hk * D * esz * n_layer
+    n_sets = max(1, math.ceil(min_bytes / alloc))
     g = torch.Generator(device=dev).manual_seed(1234)
     sets = []
     for _ in range(n_sets):
@@ -52,8 +64,13 @@ def decode_workload(torch, A, H, Hk, D, L, n_layer, dt, min_bytes):
         v = torch.randn(n_layer, L, Hk * D, generator=g, device=dev).to(dt)
         q = torch.randn(n_layer, 1, H, D, generator=g, device=dev)
         sets.append((q, k, v))
+    if first is not None:
+        sets[0][0][0].copy_(first[0].view(1, H, D))
+        sets[0][1][0].copy_(first[1])
+        sets[0][2][0].copy_(first[2])
     lens = torch.tensor([L], dtype=torch.int32, device=dev)
-    ws = A.new_decode_workspace(1, H, Hk, D, L)
+    nws = max(A.decode_workspace_bytes(1, H, Hk, D, L, w) for w in set(windows))
+    ws = torch.zeros(max(nws, 256), dtype=torch.uint8, device=dev)
     out = torch.empty(n_layer, 1, H, D, device=dev)
     scale = 1.0 / math.sqrt(D)
 
@@ -62,8 +79,8 @@ def decode_workload(torch, A, H, Hk, D, L, n_layer, dt, min_bytes):
         for li in range(n_layer):
             if events is not None:
                 events[li][0].record()
-            A.attn_decode(q[li], k[li], v[li], lens, L, Hk, scale=scale, out=out[li],
-                          workspace=ws)
+            A.attn_decode(q[li], k[li], v[li], lens, L, Hk, window=windows[li], scale=scale,
+                          out=out[li], workspace=ws)
             if events is not None:
                 events[li][1].record()
 
@@ -86,6 +103,13 @@ def decode_workload(torch, A, H, Hk, D, L, n_layer, dt, min_bytes):
                 n_sets=n_sets, out=out, n_layer=n_layer)
 
 
+def first_layer_out(torch, wl):
+    """Output of layer 0 of set 0 after an eager pass (the synth layer)."""
+    wl["step_eager"](0)
+    torch.cuda.synchronize()
+    return wl["out"][0].reshape(-1).cpu().numpy()
+
+
 def time_graph_steps(torch, wl, steps, warmup):
     graphs, n = wl["graphs"], wl["n_sets"]
     for i in range(warmup):
@@ -103,27 +127,38 @@ def time_graph_steps(torch, wl, steps, warmup):
     return t0.elapsed_time(t1) / steps, wall
 
 
-def bench_decode(torch, A, args, H, Hk, D, L, n_layer, dt, label):
-    wl = decode_workload(torch, A, H, Hk, D, L, n_layer, dt, 2 * MALL_BYTES)
+def bench_decode(torch, A, args, H, Hk, D, L, n_layer, dt, label, windows=None, first=None):
+    wl = decode_workload(torch, A, H, Hk, D, L, n_layer, dt, 2 * MALL_BYTES, windows, first)
     ms_step, wall = time_graph_steps(torch, wl, args.steps, args.warmup)
     # One decode-attention op per layer = the split-KV kernel plus its merge
     # kernel, back to back in the graph; events bracket the whole timed region
     # on the stream the graphs run on.
     us_layer = ms_step * 1000.0 / n_layer
-    lb = wl["layer_bytes"]
-    return dict(label=label, ms_per_step=ms_step, us_per_layer=us_layer,
-                gbps_step=lb / (us_layer * 1e3), layer_bytes=lb, n_sets=wl["n_sets"],
-                wall_s=wall)
+    lb = sum(wl["layer_bytes"]) / n_layer  # mean algorithmic bytes per layer
+    res = dict(label=label, ms_per_step=ms_step, us_per_layer=us_layer,
+               gbps_step=lb / (us_layer * 1e3), layer_bytes=lb, n_sets=wl["n_sets"],
+               wall_s=wall, step_bytes=sum(wl["layer_bytes"]))
+    if first is not None:
+        res["first_out"] = first_layer_out(torch, wl)
+    del wl
+    torch.cuda.empty_cache()
+    return res
 
 
-def bench_prefill(torch, A, args, S, H, Hk, D, dt):
+def bench_prefill(torch, A, args, S, H, Hk, D, dt, window=0, first=None):
+    """Causal prefill of S rows, timed as a graph of back-to-back launches.
+    first: (q, K, V) CPU tensors to run instead of torch-random inputs (the
+    SplitMix64 inputs the CPU baseline runs too); their output is returned."""
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(99)
-    q = torch.randn(S, H * D, generator=g, device=dev).to(dt)
-    k = torch.randn(S, Hk * D, generator=g, device=dev).to(dt)
-    v = torch.randn(S, Hk * D, generator=g, device=dev).to(dt)
+    if first is not None:
+        q, k, v = (t.to(dev) for t in first)
+    else:
+        q = torch.randn(S, H * D, generator=g, device=dev).to(dt)
+        k = torch.randn(S, Hk * D, generator=g, device=dev).to(dt)
+        v = torch.randn(S, Hk * D, generator=g, device=dev).to(dt)
     out = torch.empty(S, H * D, device=dev)
-    run = lambda: A.attn_prefill(q, k, v, H, Hk, D, out=out)  # noqa: E731
+    run = lambda: A.attn_prefill(q, k, v, H, Hk, D, window=window, out=out)  # noqa: E731
     for _ in range(max(3, args.warmup)):
         run()
     torch.cuda.synchronize()
@@ -150,8 +185,13 @@ def bench_prefill(torch, A, args, S, H, Hk, D, dt):
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / (n * reps)
     n = n * reps
-    flop = 4.0 * D * H * S * (S + 1) / 2  # causal pairs only
-    return dict(ms=ms, tflops=flop / (ms * 1e-3) / 1e12, flop=flop, launches=n)
+    flop = 4.0 * D * H * S * (S + 1) / 2  # causal pairs only (window >= S here)
+    res = dict(ms=ms, tflops=flop / (ms * 1e-3) / 1e12, flop=flop, launches=n)
+    if first is not None:
+        run()
+        torch.cuda.synchronize()
+        res["out"] = out.cpu().numpy()
+    return res
 
 
 def bench_prefill_paged(torch, A, args, S, H, Hk, D, dt, page):
@@ -469,44 +509,57 @@ def bench_floor(torch, A):
     return res
 
 
-def cpu_baseline_decode(H, Hk, D, L, n_layer, budget_s=12.0):
-    """The oracle (single thread, reference schedule) on layers of the same shape."""
+def synth_decode_layer(torch, H, Hk, D, L, dt, seed):
+    """One decode layer from SplitMix64 (ullm_amd.synth): q [H*D] f32, K/V
+    [L, Hk*D] rounded to the cache dtype.  The GPU bench runs it as its first
+    layer and the CPU baseline runs the very same values."""
+    from ullm_amd import synth
+
+    return (synth.randn(seed, 1, (H * D,)), synth.randn(seed, 2, (L, Hk * D), dt),
+            synth.randn(seed, 3, (L, Hk * D), dt))
+
+
+def cpu_baseline_decode(layer, H, Hk, D, L, budget_s=12.0, window=0):
+    """The oracle (single thread, the reference's serial schedule) on the
+    synth layer, repeated for about budget_s seconds."""
     import numpy as np
 
     from oracle import oracle as ora
 
-    rng = np.random.default_rng(7)
-    kc = rng.standard_normal((L, Hk * D), dtype=np.float32).astype(np.float16).astype(np.float32)
-    vc = rng.standard_normal((L, Hk * D), dtype=np.float32).astype(np.float16).astype(np.float32)
-    q = rng.standard_normal(H * D, dtype=np.float32)
+    q = layer[0].numpy().astype(np.float32)
+    kc = layer[1].float().numpy()
+    vc = layer[2].float().numpy()
     scale = 1.0 / math.sqrt(D)
     done, t0 = 0, time.perf_counter()
+    ref = None
     while time.perf_counter() - t0 < budget_s:
-        ora.attn_decode(q, kc, vc, L - 1, H, Hk, D, scale)
+        ref = ora.attn_decode(q, kc, vc, L - 1, H, Hk, D, scale, window=window)
         done += 1
     el = time.perf_counter() - t0
-    return dict(value=el / done * 1e6, unit="us/layer", cores=1, kind="port",
-                sample=f"{done} layer(s) of the cfg2 decode shape on 1 thread "
-                       f"({el:.1f} s), oracle/ref_attention.c -O2")
+    return dict(value=el / done * 1e6, layers=done, seconds=el, ref=ref)
 
 
-def cpu_baseline_prefill(S, H, Hk, D, n_rows=160):
-    import numpy as np
-
+def cpu_baseline_prefill(first, S, H, Hk, D):
+    """The oracle's full causal prefill over the synth inputs (every row of
+    every head), single thread."""
     from oracle import oracle as ora
 
-    rng = np.random.default_rng(8)
-    q = rng.standard_normal((S, H * D), dtype=np.float32)
-    kc = rng.standard_normal((S, Hk * D), dtype=np.float32)
-    vc = rng.standard_normal((S, Hk * D), dtype=np.float32)
-    rows = [int(r) for r in np.linspace(0, S - 1, n_rows)]
+    q, k, v = (t.float().numpy() for t in first)
     t0 = time.perf_counter()
-    ora.attn_prefill(q, kc, vc, S, 0, H, Hk, D, 1.0 / math.sqrt(D), rows=rows)
+    ref = ora.attn_prefill(q, k, v, S, 0, H, Hk, D, 1.0 / math.sqrt(D))
     el = time.perf_counter() - t0
-    flop = sum(4.0 * D * H * (r + 1) for r in rows)
-    rate = flop / el
-    full = 4.0 * D * H * S * (S + 1) / 2
-    return dict(gflops=rate / 1e9, est_full_ms=full / rate * 1e3, rows=n_rows, seconds=el)
+    flop = 4.0 * D * H * S * (S + 1) / 2
+    return dict(ms=el * 1e3, gflops=flop / el / 1e9, ref=ref)
+
+
+def parity(out, ref):
+    """max-abs and rel-L2 of the GPU output against the oracle's."""
+    import numpy as np
+
+    o = np.asarray(out, dtype=np.float64).reshape(-1)
+    r = np.asarray(ref, dtype=np.float64).reshape(-1)
+    return dict(max_abs=float(np.max(np.abs(o - r))),
+                rel_l2=float(np.linalg.norm(o - r) / max(np.linalg.norm(r), 1e-30)))
 
 
 def load_traffic():
@@ -534,34 +587,59 @@ def main():
     if args.only == "floor":
         print(json.dumps(bench_floor(torch, A)))
         return
+    want = lambda k: args.only in ("all", k)  # noqa: E731
     res = {}
-    if args.only in ("all", "decode"):
-        res["cfg2"] = bench_decode(torch, A, args, 12, 2, 128, 4096, 28, torch.float16, "cfg2")
-    if args.only in ("all", "prefill"):
-        res["cfg3"] = bench_prefill(torch, A, args, 2048, 32, 8, 128, torch.bfloat16)
+    # Layer 0 of the cfg2 run and the cfg3 prefill inputs come from SplitMix64
+    # (ullm_amd.synth), so the CPU baseline runs exactly what the GPU ran.
+    syn2 = synth_decode_layer(torch, 12, 2, 128, 4096, torch.float16, seed=2)
+    syn3 = None
+    if want("decode"):
+        res["cfg2"] = bench_decode(torch, A, args, 12, 2, 128, 4096, 28, torch.float16, "cfg2",
+                                   first=syn2)
+    if want("prefill"):
+        from ullm_amd import synth
+
+        syn3 = tuple(synth.randn(3, t, (2048, n * 128), torch.bfloat16)
+                     for t, n in ((1, 32), (2, 8), (3, 8)))
+        res["cfg3"] = bench_prefill(torch, A, args, 2048, 32, 8, 128, torch.bfloat16, first=syn3)
         res["cfg3_paged"] = bench_prefill_paged(torch, A, args, 2048, 32, 8, 128, torch.bfloat16,
                                                 256)
-    if args.only in ("all", "append"):
+    if want("cfg1"):
+        res["cfg1"] = bench_decode(torch, A, args, 32, 8, 64, 512, 28, torch.float32, "cfg1")
+    if want("cfg4"):
+        # One step = a 6-layer group: 5 sliding-window layers (1024 keys) and
+        # the global layer, at context 8192 (forward.rs:450-454 / lib.rs:1183-1186).
+        res["cfg4"] = bench_decode(torch, A, argparse.Namespace(steps=max(10, args.steps // 4),
+                                                                warmup=3),
+                                   8, 4, 256, 8192, 6, torch.float16, "cfg4",
+                                   windows=[1024] * 5 + [0])
+        res["cfg4_prefill"] = bench_prefill(torch, A, args, 1024, 8, 4, 256, torch.float16,
+                                            window=1024)
+    if want("append"):
         res["append"] = bench_append(torch, A, args, 2048, 32, 8, 128, torch.bfloat16)
-    if args.only in ("all", "proj"):
+    if want("proj"):
         res["proj"] = bench_proj(torch, A, args, 2560, 32, 8, 128, torch.bfloat16)
-    if args.only in ("all", "matmul"):
+    if want("matmul"):
         res["matmul"] = bench_matmul(torch, A, args, 2048, 2560, (4096, 1024, 1024))
-    if args.only in ("all", "paged"):
+    if want("paged"):
         res["paged"] = bench_paged(torch, A, args, 32, 4, 128, 8, 4096, 32768, 48, 256,
                                    torch.bfloat16)
-    if args.only in ("all", "long"):
+    if want("long"):
         res["cfg5"] = bench_decode(torch, A, argparse.Namespace(steps=max(5, args.steps // 10),
                                                                 warmup=3),
                                    32, 4, 128, 32768, 48, torch.bfloat16, "cfg5")
-    if args.only in ("all",):
+    if args.only == "all":
         res["floor"] = bench_floor(torch, A)
     if args.only != "all":
+        for r in res.values():
+            r.pop("first_out", None)
+            r.pop("out", None)
         print(json.dumps(res))
         return
 
     d, p, lc, ap, pj = res["cfg2"], res["cfg3"], res["cfg5"], res["append"], res["proj"]
     mm, pg = res["matmul"], res["paged"]
+    c1, c4, c4p = res["cfg1"], res["cfg4"], res["cfg4_prefill"]
     traffic = load_traffic()
     line = {
         "metric": METRIC,
@@ -580,18 +658,42 @@ def main():
             "workload": "cfg2 Qwen2.5-1.5B-shaped decode attention: batch 1, 12 q heads, "
                         "2 kv heads, head_dim 128, f16 KV cache 4096, 28 layers per step "
                         "(HIP graph per step, KV sets rotated over "
-                        f"{d['n_sets']} x 28 layers to defeat the MALL)",
+                        f"{d['n_sets']} x 28 layers to defeat the MALL; layer 0 of set 0 is "
+                        "SplitMix64 data, the rest torch-random)",
             "batch": 1, "n_head": 12, "n_kv_head": 2, "head_dim": 128, "ctx": 4096,
             "layers": 28, "kv_dtype": "f16",
         },
         "decode_gbps": round(d["gbps_step"], 1),
         "prefill": {"workload": "cfg3 Qwen3-4B-shaped causal prefill, S=2048, 32/8 heads, "
-                                "head_dim 128, bf16", "ms": round(p["ms"], 4),
+                                "head_dim 128, bf16 (SplitMix64 inputs)", "ms": round(p["ms"], 4),
                     "tflops": round(p["tflops"], 2),
                     "flop_causal": p["flop"],
                     "paged": {"page": res["cfg3_paged"]["page"],
                               "ms": round(res["cfg3_paged"]["ms"], 4),
                               "tflops": round(res["cfg3_paged"]["tflops"], 2)}},
+        "cfg1_decode": {"workload": "cfg1 Llama-3.2-1B-shaped decode: 32/8 heads, head_dim 64, "
+                                    "f32 KV 512, 28 layers per graph (rotated past the MALL)",
+                        "kernel": "decode_split_kernel (f32 VALU) + decode_merge_kernel",
+                        "us_per_layer": round(c1["us_per_layer"], 3),
+                        "algorithmic_bytes": int(c1["layer_bytes"]),
+                        "gbps": round(c1["gbps_step"], 1),
+                        "frac_hbm": round(c1["gbps_step"] / HBM_PEAK_GBS, 4)},
+        "cfg4_decode": {"workload": "cfg4 Gemma-3-4B-shaped decode group: 8/4 heads, head_dim "
+                                    "256, f16 KV, context 8192; 6 layers per step = 5 sliding-"
+                                    "window layers (1024 keys) + 1 global layer, rotated past "
+                                    "the MALL",
+                        "kernel": "decode_mfma_kernel<F16,256> + decode_merge_kernel",
+                        "us_per_group": round(c4["ms_per_step"] * 1e3, 3),
+                        "us_per_layer": round(c4["us_per_layer"], 3),
+                        "algorithmic_bytes_per_group": int(c4["step_bytes"]),
+                        "gbps": round(c4["gbps_step"], 1),
+                        "frac_hbm": round(c4["gbps_step"] / HBM_PEAK_GBS, 4)},
+        "cfg4_prefill": {"workload": "cfg4 causal prefill, S=1024, 8/4 heads, head_dim 256, "
+                                     "f16, window 1024 (= causal at this length)",
+                         "kernel": "prefill_sk_kernel<F16,256>",
+                         "ms": round(c4p["ms"], 4), "tflops": round(c4p["tflops"], 2),
+                         "flop_causal": c4p["flop"],
+                         "frac_mfma": round(c4p["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)},
         "long_decode": {"workload": "cfg5 Qwen3-30B-A3B-shaped decode, 32/4 heads, head_dim "
                                     "128, bf16 KV 32768, 48 layers",
                         "us_per_layer": round(lc["us_per_layer"], 3),
@@ -636,9 +738,10 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["gbps_step"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("bytes_per_launch") if traffic else None,
-                     "kernel": "decode_dma_kernel<F16,128,1> + decode_merge_kernel<128,4> "
+                     "traffic_measured_at": traffic.get("commit") if traffic else None,
+                     "kernel": "decode_dma_kernel<F16,128,1> + decode_merge_kernel<128,2> "
                                "(one decode-attention op per layer)",
-                     "algorithmic_bytes": d["layer_bytes"],
+                     "algorithmic_bytes": int(d["layer_bytes"]),
                      "us_per_launch": round(d["us_per_layer"], 3),
                      "read_floor": {
                          "note": "ullm_hip_stream_read of the same 4 MiB as one graph node: the "
@@ -652,18 +755,60 @@ def main():
                              "kernel": "prefill4_kernel<BF16,128>"},
     }
     if not args.no_cpu:
-        cb = cpu_baseline_decode(12, 2, 128, 4096, 28)
-        cp = cpu_baseline_prefill(2048, 32, 8, 128)
-        cb["prefill_sample"] = (f"{cp['rows']} rows x 32 heads of cfg3 in {cp['seconds']:.1f} s:"
-                                f" {cp['gflops']:.2f} GFLOP/s, full prefill est. "
-                                f"{cp['est_full_ms']:.0f} ms")
-        cb["host_cpu"] = _cpu_model()
-        cb["nproc"] = os.cpu_count()
-        line["cpu_baseline"] = cb
+        # The oracle on rank 0's host, one thread (the reference's attention
+        # loop is serial, lib.rs:917-938), on the SplitMix64 layer the GPU ran
+        # as layer 0: about 12 s of repeated layers, then the full cfg3 prefill.
+        cd = cpu_baseline_decode(syn2, 12, 2, 128, 4096)
+        cp = cpu_baseline_prefill(syn3, 2048, 32, 8, 128)
+        line["cpu_baseline"] = {
+            "value": round(cd["value"], 1), "unit": "us/layer", "cores": 1, "kind": "port",
+            "sample": f"{cd['layers']} repetitions of the cfg2 SplitMix64 layer (the GPU run's "
+                      f"layer 0) in {cd['seconds']:.1f} s on 1 thread, oracle/ref_attention.c "
+                      f"-O2; then the full cfg3 prefill (all 2048 rows x 32 heads, the GPU run's "
+                      f"SplitMix64 inputs) in {cp['ms']:.0f} ms = {cp['gflops']:.2f} GFLOP/s",
+            "prefill_ms": round(cp["ms"], 1),
+            "prefill_gflops": round(cp["gflops"], 3),
+            "host_cpu": _cpu_model(),
+            "host_cpu_id": _cpu_id(),
+            "nproc": os.cpu_count(),
+        }
+        # The same inputs through the GPU path: its output against the oracle's.
+        line["parity"] = {"cfg2_layer0": parity(d["first_out"], cd["ref"]),
+                          "cfg3_prefill": parity(p["out"], cp["ref"]),
+                          "tolerance": {"max_abs": 2e-3, "rel_l2": 1e-3}}
     print(json.dumps(line))
 
 
+def _cpu_id():
+    """lscpu's vendor / family / model / stepping (the model name alone can be
+    generic on a virtualised host)."""
+    import subprocess
+
+    keys = ("Vendor ID", "CPU family", "Model", "Stepping", "Thread(s) per core",
+            "Core(s) per socket", "Socket(s)")
+    out = {}
+    try:
+        r = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10)
+        for ln in r.stdout.splitlines():
+            k, _, v = ln.partition(":")
+            if k.strip() in keys:
+                out[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return out
+
+
 def _cpu_model():
+    """The host CPU's model name, as lscpu reports it (/proc/cpuinfo otherwise)."""
+    import subprocess
+
+    try:
+        r = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10)
+        for ln in r.stdout.splitlines():
+            if ln.strip().startswith("Model name:"):
+                return ln.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
