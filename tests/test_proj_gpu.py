@@ -108,3 +108,41 @@ def test_split_counters_reset_between_calls(dev):
     for seed in (7, 8, 9):
         run_case(dev, 1, 100, 12, 2, 128, 1536, "bf16", 128, True, norm=True, bias=False,
                  qdt="f32", kvdt="bf16", seed=seed)
+
+
+def test_split_exchange_2000_calls_repeat_exactly(dev):
+    """The split projection's cross-workgroup exchange under load: 2000
+    back-to-back calls at the Qwen3-4B decode shape on one workspace, each
+    call's q (written to its own row) and the final K/V row bit-identical to
+    the first call's; a stale part reloaded by the last arriver would change
+    a head.  Stops at the first mismatching call."""
+    H, Hk, D, hidden, n = 32, 8, 128, 2560, 2000
+    print(f"[proj] exchange repeat x{n}", flush=True)
+    x = synth.randn(21, 1, (1, hidden)).to(dev)
+    sd = 1.0 / np.sqrt(hidden)
+    wq, wk, wv = ((synth.randn(21, t, (m * D, hidden)) * sd).to(torch.bfloat16).to(dev)
+                  for t, m in ((2, H), (3, Hk), (4, Hk)))
+    qn = (synth.randn(21, 5, (D,)) * 0.2 + 1.0).to(dev)
+    kn = (synth.randn(21, 6, (D,)) * 0.2 + 1.0).to(dev)
+    cs = A.rope_table(4096, D, 1e6, device=dev)
+    kc = torch.zeros(4096, Hk * D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    ws = torch.zeros(int(A.L.lib().ullm_hip_qkv_proj_workspace_bytes(1, H, Hk, D)),
+                     dtype=torch.uint8, device=dev)
+    assert ws.numel() > 0, "the decode shape must take the split path"
+    qs = torch.empty(n, 1, H * D, device=dev)
+    kv0 = None
+    for i in range(n):
+        A.qkv_proj_append(x, wq, wk, wv, kc, vc, cs, start_pos=4095, n_head=H, n_kv_head=Hk,
+                          head_dim=D, q_norm=qn, k_norm=kn, q_out=qs[i], workspace=ws)
+        if i == 0:
+            torch.cuda.synchronize()
+            kv0 = (kc[4095].clone(), vc[4095].clone())
+    torch.cuda.synchronize()
+    same = (qs == qs[0]).all(dim=2).reshape(-1).cpu()
+    bad = (~same).nonzero()
+    assert bad.numel() == 0, f"call {int(bad[0])} differs from call 0"
+    assert torch.equal(kc[4095], kv0[0]) and torch.equal(vc[4095], kv0[1])
+    # the first call is right, too
+    ref = qs[0].cpu().numpy()
+    assert np.isfinite(ref).all() and np.abs(ref).max() > 0

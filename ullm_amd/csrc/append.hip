@@ -20,6 +20,13 @@
 #include "common.hpp"
 #include "mfma_util.hpp"
 #include "wave.hpp"
+// The split projection's cross-workgroup exchange (qkv_proj_kernel) relies
+// on gfx950's cache policy for system-scope stores and on its L2 topology;
+// this library is built for gfx950 only.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "append.hip: the split projection exchange is written for gfx950"
+#endif
+
 
 namespace ullm {
 
@@ -342,13 +349,26 @@ __global__ __launch_bounds__(kProjWaves * 64) void qkv_proj_kernel(
         // NSP workgroups share a head vector: wave 0 of each stores its part
         // to the workspace and counts itself in; the last to arrive reads
         // the whole vector back, finishes the head and resets the counter
-        // for the next call.  The parts travel by system-coherent accesses
-        // (sc0 sc1: stores written through to memory, loads served from
-        // it), so no L2 write-back or invalidate is needed: each part's
-        // stores have completed (vmcnt(0)) before its counter increment, and
-        // the last arriver's loads bypass its XCD's L2.  An agent-scope
-        // acquire-release counter (L2 write-back and invalidate) measured
-        // 12.4 us against 10.9 us at the Qwen3-4B decode shape.
+        // for the next call.  Nobody waits, so no co-residency is assumed.
+        //
+        // Ordering (LLVM AMDGPU memory model, gfx950: one L2 per XCD, the
+        // L2s not coherent with each other for ordinary accesses):
+        //  * the parts are system-scope atomic stores, which gfx950 issues
+        //    with sc0 sc1: written through every cache level to memory;
+        //  * `s_waitcnt vmcnt(0)` completes them before the counter update is
+        //    issued, so they are performed at memory before the count is.
+        //    This is the agent-scope release sequence (`buffer_wbl2 sc1;
+        //    s_waitcnt vmcnt(0)`) minus the L2 write-back, which has nothing
+        //    of this exchange to write back: the parts never sit dirty in an
+        //    L2.  The write-back would cost 1.5 us per call at the Qwen3-4B
+        //    decode shape (12.4 against 10.9 us, acquire-release counter);
+        //  * the counter is an agent-scope atomic, performed at memory;
+        //  * only the last arriver, having read n - 1, issues the agent-scope
+        //    ACQUIRE fence (`buffer_inv sc1`: its CU's L1 and its XCD's L2
+        //    drop their lines) before it reloads the parts, so no stale copy
+        //    can serve them.
+        // The workspace is zeroed once by the caller; every call leaves its
+        // counters at zero.
         constexpr int PART = D / NSP;
         float *yh = ws_y + ((int64_t)row * slots + slot) * D;
         for (int i = lane; i < PART; i += 64)
@@ -363,8 +383,9 @@ __global__ __launch_bounds__(kProjWaves * 64) void qkv_proj_kernel(
         }
         prev = __builtin_amdgcn_readfirstlane(prev);
         if (prev != NSP - 1) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         for (int i = lane; i < D; i += 64)
-            ys[i] = __hip_atomic_load(yh + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            ys[i] = __hip_atomic_load(yh + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_wave_barrier();
     }
     const int pos = start_pos + row;
