@@ -83,6 +83,29 @@ int ullm_hip_attn_decode(const float *q, const void *k_cache, const void *v_cach
                          int head_dim, float scale, float *out, void *workspace,
                          size_t workspace_bytes, void *stream);
 
+/* ullm_hip_attn_decode without a workspace and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and result as
+ * ullm_hip_attn_decode, minus the workspace: the split-KV partials live in a
+ * static device array of ullm_hip_decode_noalloc_max_bytes() bytes per GPU
+ * (4 MiB), held by every GPU the library runs on until the process ends.
+ * A shape whose partials exceed it returns ULLM_HIP_E_WORKSPACE (batch 1
+ * covers every config up to 32 query heads at head_dim 128 and 32K keys).
+ * The first call on a device resolves the array's address (no allocation).
+ * All calls on one GPU share that array: calls that overlap on one GPU
+ * (different streams, or host threads) race and must be serialised by the
+ * caller.  Nothing needs clearing between calls (every partial is written
+ * before it is read). */
+int ullm_hip_attn_decode_noalloc(const float *q, const void *k_cache, const void *v_cache,
+                                 int kv_dtype, int64_t kv_stride, int64_t seq_stride,
+                                 const int32_t *seq_lens, int max_len, int window, int batch,
+                                 int n_head, int n_kv_head, int head_dim, float scale, float *out,
+                                 void *stream);
+
+/* Bytes of the static scratch behind ullm_hip_attn_decode_noalloc. */
+size_t ullm_hip_decode_noalloc_max_bytes(void);
+
 /* Causal multi-token prefill attention on MFMA.
  * Replaces attn_flash_batch (crates/ullm-metal/src/forward.rs:855-858,
  * :1116-1147; shader.metal:1030-1074) and computes what the CPU reference

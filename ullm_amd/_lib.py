@@ -23,6 +23,10 @@ SIGNATURES = {
         _i,
         [_vp, _vp, _vp, _i, _i64, _i64, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _vp, _sz, _vp],
     ),
+    "ullm_hip_attn_decode_noalloc": (
+        _i, [_vp, _vp, _vp, _i, _i64, _i64, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _vp],
+    ),
+    "ullm_hip_decode_noalloc_max_bytes": (_sz, []),
     "ullm_hip_attn_prefill": (
         _i, [_vp, _vp, _vp, _i, _i64, _i, _i, _i, _i, _i, _i, _f, _vp, _vp]
     ),

@@ -25,6 +25,7 @@
 #include "wave.hpp"
 #include <cstdlib>
 #include <algorithm>
+#include <mutex>
 
 namespace ullm {
 
@@ -432,3 +433,73 @@ int decode_f32_paged(const float *q, const void *kp, const void *vp, int64_t kvs
 
 }  // namespace ullm
 
+
+// ---------------------------------------------------------------------------
+// Decode without any allocation: the split partials live in a file-scope
+// device array instead of a caller workspace.  No counterpart in the
+// reference; for callers that cannot allocate (code under HIP graph capture,
+// tight serving loops, harnesses that forbid hipMalloc).
+namespace ullm {
+
+constexpr size_t kScratchBytes = (size_t)4 << 20;
+// One copy per GPU, held until the process ends.  In host code `scratch` is
+// only a handle: its device address (per device) comes from
+// hipGetSymbolAddress and is what kernels and copies receive.
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void *g_scratch_addr[kMaxDevices];
+static std::once_flag g_scratch_once[kMaxDevices];
+static hipError_t g_scratch_err[kMaxDevices];
+
+// The device address of `scratch` on the current device, resolved once per
+// device (with that device current) on its first call.
+static int scratch_address(void **out) {
+    int dev = -1;
+    int rc = check_hip(hipGetDevice(&dev), "decode_noalloc: hipGetDevice");
+    if (rc) return rc;
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "decode_noalloc: device %d beyond %d", dev,
+                         kMaxDevices);
+    std::call_once(g_scratch_once[dev], [dev] {
+        void *p = nullptr;
+        g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_addr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+    });
+    if (g_scratch_err[dev] != hipSuccess)
+        return check_hip(g_scratch_err[dev], "decode_noalloc: hipGetSymbolAddress(scratch)");
+    *out = g_scratch_addr[dev];
+    return ULLM_HIP_OK;
+}
+
+}  // namespace ullm
+
+extern "C" size_t ullm_hip_decode_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" int ullm_hip_attn_decode_noalloc(const float *q, const void *k_cache,
+                                            const void *v_cache, int kv_dtype, int64_t kv_stride,
+                                            int64_t seq_stride, const int32_t *seq_lens,
+                                            int max_len, int window, int batch, int n_head,
+                                            int n_kv_head, int head_dim, float scale, float *out,
+                                            void *stream) {
+    int rc = validate_decode(kv_dtype, kv_stride, max_len, batch, n_head, n_kv_head, head_dim);
+    if (rc) return rc;
+    // This call's partials (its own plan, not the bound over shorter calls).
+    const size_t need =
+        kv_dtype == ULLM_DT_F32
+            ? plan_decode(batch, n_head, n_kv_head, head_dim, kv_dtype, max_len, window).bytes
+            : decode_mfma_plan_bytes(batch, n_head, n_kv_head, head_dim, max_len, window);
+    if (need > kScratchBytes)
+        return set_error(ULLM_HIP_E_WORKSPACE,
+                         "decode_noalloc: this shape needs %zu bytes of split partials, above the "
+                         "%zu-byte static scratch; use ullm_hip_attn_decode with a workspace",
+                         need, kScratchBytes);
+    void *ws = nullptr;
+    if (need > 0) {
+        rc = scratch_address(&ws);
+        if (rc) return rc;
+    }
+    return ullm_hip_attn_decode(q, k_cache, v_cache, kv_dtype, kv_stride, seq_stride, seq_lens,
+                                max_len, window, batch, n_head, n_kv_head, head_dim, scale, out,
+                                ws, need > 0 ? kScratchBytes : 0, stream);
+}

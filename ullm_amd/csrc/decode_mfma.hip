@@ -903,6 +903,11 @@ static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const
     if (p.splits > 1) launch_merge<D>(p, batch, nh, out, ws, st);
 }
 
+size_t decode_mfma_plan_bytes(int batch, int n_head, int n_kv_head, int D, int max_len,
+                              int window) {
+    return plan_mfma(batch, n_head, n_kv_head, D, max_len, window).bytes;
+}
+
 int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64_t kvs,
                 int64_t ss, const int32_t *lens, int max_len, int win, int batch, int nh,
                 int nkv, int D, float qs, float *out, void *ws, size_t ws_bytes,
