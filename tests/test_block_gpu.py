@@ -82,3 +82,45 @@ def test_prefill_then_decode_block(dev, wdt, kvdt, D, window):
         ref_d = ora.attn_decode(qp[pos].copy(), kc[:pos + 1], vc[:pos + 1], pos, H, Hk, D, scale,
                                 window=window)
         assert_close(outs_d[i], ref_d, what=f"decode block pos {pos}", **tol)
+
+
+def test_forward_debug_reports_every_op(dev):
+    """GpuAttention.forward_debug (the attention half of the reference's
+    GpuForward::forward_debug, forward.rs:530-635): one report line per op,
+    all clean on finite inputs, the same attention output and cache row as
+    forward_proj; a NaN in the hidden state shows up from the projections
+    on."""
+    n_embd, H, Hk, D, pos = 512, 8, 2, 128, 37
+    p = A.AttnParams(n_layer=1, n_head=H, n_kv_head=Hk, head_dim=D, n_ctx=64, rope_theta=1e6,
+                     kv_dtype=torch.bfloat16)
+    sd = 1.0 / math.sqrt(n_embd)
+    w = [(synth.randn(12, t, (n * D, n_embd)) * sd).to(torch.bfloat16).to(dev)
+         for t, n in ((1, H), (2, Hk), (3, Hk))]
+    qn = (synth.randn(12, 4, (D,)) * 0.2 + 1.0).to(dev)
+    kn = (synth.randn(12, 5, (D,)) * 0.2 + 1.0).to(dev)
+    qb = (synth.randn(12, 6, (H * D,)) * 0.1).to(dev)
+    kb = (synth.randn(12, 7, (Hk * D,)) * 0.1).to(dev)
+    vb = (synth.randn(12, 8, (Hk * D,)) * 0.1).to(dev)
+    x = synth.randn(12, 9, (n_embd,)).to(dev)
+    kw = dict(q_norm=qn, k_norm=kn, q_bias=qb, k_bias=kb, v_bias=vb)
+    a, b = A.GpuAttention(p, device=dev), A.GpuAttention(p, device=dev)
+    # earlier positions hold the same random rows in both caches
+    a.key_cache.copy_(synth.randn(12, 10, tuple(a.key_cache.shape), torch.bfloat16))
+    a.val_cache.copy_(synth.randn(12, 11, tuple(a.val_cache.shape), torch.bfloat16))
+    b.key_cache.copy_(a.key_cache)
+    b.val_cache.copy_(a.val_cache)
+    out, rep = a.forward_debug(x, pos, *w, **kw, log=False)
+    want = b.forward_proj(0, x, pos, *w, **kw)
+    torch.cuda.synchronize()
+    labels = [r[0] for r in rep]
+    assert labels == ["attn_in", "wq", "wk", "wv", "bias_q", "bias_k", "bias_v", "q_norm",
+                      "k_norm", "rope_q", "rope_k", "attn_out"], labels
+    assert all(r[1] == 0 and r[2] == 0 and r[3] > 0 for r in rep), rep
+    assert_close(out.cpu().numpy(), want.cpu().numpy(), max_abs=1e-5, rel_l2=1e-6,
+                 what="debug vs forward_proj")
+    assert torch.equal(a.key_cache[0, pos], b.key_cache[0, pos])
+    xn = x.clone()
+    xn[3] = float("nan")
+    _, rep = a.forward_debug(xn, pos, *w, **kw, log=False)
+    nan = {r[0]: r[1] for r in rep}
+    assert nan["attn_in"] == 1 and nan["wq"] == H * D and nan["attn_out"] > 0

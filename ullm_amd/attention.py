@@ -363,7 +363,28 @@ class GpuAttention:
         self.rope_cs = rope_table(p.n_ctx, self.rotary_dim, p.rope_theta, device=self.device)
         self.workspace = new_decode_workspace(1, p.n_head, p.n_kv_head, p.head_dim, p.n_ctx,
                                               0, self.device)
-        self._len = torch.zeros(1, dtype=torch.int32, device=self.device)
+        # seq_lens for every position, uploaded once: decoding at pos passes
+        # the device slice holding pos + 1 (no per-token copy or fill, nothing
+        # for a captured graph to replay but kernels), and an f32-cache prefill
+        # at start_pos passes the S consecutive lengths from start_pos + 1.
+        self._lens = torch.arange(1, p.n_ctx + 1, dtype=torch.int32, device=self.device)
+        self._batch_ws = {}
+
+    def _rows_decode(self, layer, qr, start_pos, S):
+        """f32-cache prefill: the S query rows as S ragged "sequences" over the
+        shared cache (seq_stride 0), lengths start_pos + 1 .. start_pos + S."""
+        p = self.p
+        key = (S, start_pos + S, self._window(layer))
+        ws = self._batch_ws.get(key)
+        if ws is None:
+            ws = new_decode_workspace(S, p.n_head, p.n_kv_head, p.head_dim, start_pos + S,
+                                      self._window(layer), self.device)
+            self._batch_ws[key] = ws
+        out = attn_decode(qr.view(S, p.n_head, p.head_dim), self.key_cache[layer],
+                          self.val_cache[layer], self._lens[start_pos:start_pos + S],
+                          start_pos + S, p.n_kv_head, window=self._window(layer),
+                          scale=self.scale, seq_stride=0, workspace=ws)
+        return out.view(S, -1)
 
     def supports_batched_prefill(self) -> bool:
         """Prefill runs on MFMA for f16/bf16 caches; an f32 cache takes the
@@ -393,9 +414,8 @@ class GpuAttention:
             raise L.UllmHipError(L.E_INVALID, f"pos {pos} outside the context")
         qr = self._append(layer, q.view(1, -1), k.view(1, -1), v.view(1, -1), pos,
                           torch.float32, (q_norm, k_norm), (q_bias, k_bias, v_bias))
-        self._len.fill_(pos + 1)
         out = attn_decode(qr.view(1, p.n_head, p.head_dim), self.key_cache[layer],
-                          self.val_cache[layer], self._len, pos + 1, p.n_kv_head,
+                          self.val_cache[layer], self._lens[pos:pos + 1], pos + 1, p.n_kv_head,
                           window=self._window(layer), scale=self.scale,
                           workspace=self.workspace)
         return out.view(-1)
@@ -411,15 +431,7 @@ class GpuAttention:
         if p.kv_dtype == torch.float32:
             qr = self._append(layer, q, k, v, start_pos, torch.float32, (q_norm, k_norm),
                               (q_bias, k_bias, v_bias))
-            lens = torch.arange(start_pos + 1, start_pos + S + 1, dtype=torch.int32,
-                                device=self.device)
-            ws = new_decode_workspace(S, p.n_head, p.n_kv_head, p.head_dim, start_pos + S,
-                                      self._window(layer), self.device)
-            out = attn_decode(qr.view(S, p.n_head, p.head_dim), self.key_cache[layer],
-                              self.val_cache[layer], lens, start_pos + S, p.n_kv_head,
-                              window=self._window(layer), scale=self.scale, seq_stride=0,
-                              workspace=ws)
-            return out.view(S, -1)
+            return self._rows_decode(layer, qr, start_pos, S)
         qr = self._append(layer, q, k, v, start_pos, p.kv_dtype, (q_norm, k_norm),
                           (q_bias, k_bias, v_bias))
         return attn_prefill(qr, self.key_cache[layer], self.val_cache[layer], p.n_head,
@@ -442,9 +454,8 @@ class GpuAttention:
                              rotary_dim=self.rotary_dim, neox=p.rope_neox, q_norm=q_norm,
                              k_norm=k_norm, eps=p.eps, q_bias=q_bias, k_bias=k_bias,
                              v_bias=v_bias, q_dtype=torch.float32)
-        self._len.fill_(pos + 1)
         out = attn_decode(qr.view(1, p.n_head, p.head_dim), self.key_cache[layer],
-                          self.val_cache[layer], self._len, pos + 1, p.n_kv_head,
+                          self.val_cache[layer], self._lens[pos:pos + 1], pos + 1, p.n_kv_head,
                           window=self._window(layer), scale=self.scale,
                           workspace=self.workspace)
         return out.view(-1)
@@ -474,16 +485,94 @@ class GpuAttention:
                              k_norm=k_norm, eps=p.eps, q_bias=q_bias, k_bias=k_bias,
                              v_bias=v_bias, q_dtype=q_dtype)
         if p.kv_dtype == torch.float32:
-            lens = torch.arange(start_pos + 1, start_pos + S + 1, dtype=torch.int32,
-                                device=self.device)
-            ws = new_decode_workspace(S, p.n_head, p.n_kv_head, p.head_dim, start_pos + S,
-                                      self._window(layer), self.device)
-            out = attn_decode(qr.view(S, p.n_head, p.head_dim), self.key_cache[layer],
-                              self.val_cache[layer], lens, start_pos + S, p.n_kv_head,
-                              window=self._window(layer), scale=self.scale, seq_stride=0,
-                              workspace=ws)
-            return out.view(S, -1)
+            return self._rows_decode(layer, qr, start_pos, S)
         return attn_prefill(qr, self.key_cache[layer], self.val_cache[layer], p.n_head,
                             p.n_kv_head, p.head_dim, start_pos=start_pos,
                             window=self._window(layer), scale=self.scale)
 
+
+    # ---- numerical debugging ----
+
+    def forward_debug(self, xb, pos: int, wq, wk, wv, q_norm=None, k_norm=None, q_bias=None,
+                      k_bias=None, v_bias=None, layer: int = 0, log=True):
+        """The attention half of GpuForward::forward_debug (forward.rs:530-635):
+        layer 0's attention one op at a time from the normed hidden state xb,
+        each op its own launch followed by a synchronisation, reporting the
+        NaN count, inf count and largest finite |value| of every intermediate
+        (printed as `[dbg posP] label nan=.. inf=.. maxabs=..` when `log`, as
+        the reference prints them).  The fused kernels are run with their
+        later stages switched off to expose the intermediates: the raw
+        projections come from the fused projection at position 0 with no
+        norm or bias (RoPE at position 0 is the identity), then the bias,
+        the Q/K norms and RoPE follow as appends into scratch rows, and the
+        last append writes the cache row exactly as forward_proj does.  The
+        attention scores are never materialised by this path, so the report
+        goes from rope_k to attn_out.  Returns (attention output, report:
+        a list of (label, nan, inf, maxabs))."""
+        p = self.p
+        if not 0 <= pos < p.n_ctx:
+            raise L.UllmHipError(L.E_INVALID, f"pos {pos} outside the context")
+        report = []
+
+        def check(t, label):
+            torch.cuda.synchronize()
+            v = t.detach().float().reshape(-1).cpu()
+            nan = int(torch.isnan(v).sum())
+            inf = int(torch.isinf(v).sum())
+            fin = v[torch.isfinite(v)]
+            mx = float(fin.abs().max()) if fin.numel() else 0.0
+            report.append((label, nan, inf, mx))
+            if log:
+                import sys
+
+                print(f"[dbg pos{pos}] {label:<14} nan={nan} inf={inf} maxabs={mx:.4f}",
+                      file=sys.stderr)
+
+        dev, kd = self.device, self.kv_dim
+        x = xb.view(1, -1)
+        check(x, "attn_in")
+        # raw projections: scratch f32 K/V row 0, identity RoPE, no norm/bias
+        sk = torch.zeros(1, kd, device=dev)
+        sv = torch.zeros_like(sk)
+        q_raw = qkv_proj_append(x, wq, wk, wv, sk, sv, self.rope_cs, start_pos=0,
+                                n_head=p.n_head, n_kv_head=p.n_kv_head, head_dim=p.head_dim,
+                                rotary_dim=self.rotary_dim, neox=p.rope_neox,
+                                q_dtype=torch.float32)
+        k_raw, v_raw = sk.clone(), sv.clone()
+        check(q_raw, "wq")
+        check(k_raw, "wk")
+        check(v_raw, "wv")
+
+        def scratch_append(norms, biases, at):
+            ck = torch.zeros(at + 1, kd, device=dev)
+            cv = torch.zeros_like(ck)
+            qo = qkv_append(q_raw, k_raw, v_raw, ck, cv, self.rope_cs, start_pos=at,
+                            n_head=p.n_head, n_kv_head=p.n_kv_head, head_dim=p.head_dim,
+                            rotary_dim=self.rotary_dim, neox=p.rope_neox, q_norm=norms[0],
+                            k_norm=norms[1], eps=p.eps, q_bias=biases[0], k_bias=biases[1],
+                            v_bias=biases[2], q_dtype=torch.float32)
+            return qo, ck[at], cv[at]
+
+        biases = (q_bias, k_bias, v_bias)
+        if any(b is not None for b in biases):
+            qb_, kb_, vb_ = scratch_append((None, None), biases, 0)
+            check(qb_, "bias_q")
+            check(kb_, "bias_k")
+            check(vb_, "bias_v")
+        if q_norm is not None or k_norm is not None:
+            qn_, kn_, _ = scratch_append((q_norm, k_norm), biases, 0)
+            if q_norm is not None:
+                check(qn_, "q_norm")
+            if k_norm is not None:
+                check(kn_, "k_norm")
+        # the real append: RoPE at pos, K/V into the cache (as forward_proj)
+        qr = self._append(layer, q_raw, k_raw, v_raw, pos, torch.float32, (q_norm, k_norm),
+                          biases)
+        check(qr, "rope_q")
+        check(self.key_cache[layer, pos], "rope_k")
+        out = attn_decode(qr.view(1, p.n_head, p.head_dim), self.key_cache[layer],
+                          self.val_cache[layer], self._lens[pos:pos + 1], pos + 1, p.n_kv_head,
+                          window=self._window(layer), scale=self.scale,
+                          workspace=self.workspace)
+        check(out, "attn_out")
+        return out.view(-1), report
