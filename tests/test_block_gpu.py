@@ -87,8 +87,8 @@ def test_prefill_then_decode_block(dev, wdt, kvdt, D, window):
 def test_forward_debug_reports_every_op(dev):
     """GpuAttention.forward_debug (the attention half of the reference's
     GpuForward::forward_debug, forward.rs:530-635): one report line per op,
-    all clean on finite inputs, the same attention output and cache row as
-    forward_proj; a NaN in the hidden state shows up from the projections
+    all clean on finite inputs, the attention output and cache row of
+    forward_proj (to f32 rounding / one bf16 ulp); a NaN in the hidden state shows up from the projections
     on."""
     n_embd, H, Hk, D, pos = 512, 8, 2, 128, 37
     p = A.AttnParams(n_layer=1, n_head=H, n_kv_head=Hk, head_dim=D, n_ctx=64, rope_theta=1e6,
@@ -116,9 +116,12 @@ def test_forward_debug_reports_every_op(dev):
     assert labels == ["attn_in", "wq", "wk", "wv", "bias_q", "bias_k", "bias_v", "q_norm",
                       "k_norm", "rope_q", "rope_k", "attn_out"], labels
     assert all(r[1] == 0 and r[2] == 0 and r[3] > 0 for r in rep), rep
-    assert_close(out.cpu().numpy(), want.cpu().numpy(), max_abs=1e-5, rel_l2=1e-6,
+    # The fused projection and the separate append compute the per-head RMS
+    # sum in different lane orders: f32 rounding apart, not more.
+    assert_close(out.cpu().numpy(), want.cpu().numpy(), max_abs=2e-5, rel_l2=1e-5,
                  what="debug vs forward_proj")
-    assert torch.equal(a.key_cache[0, pos], b.key_cache[0, pos])
+    kd = (a.key_cache[0, pos].float() - b.key_cache[0, pos].float()).abs()
+    assert (kd <= 2.0**-7 * b.key_cache[0, pos].float().abs().clamp(min=1.0)).all()
     xn = x.clone()
     xn[3] = float("nan")
     _, rep = a.forward_debug(xn, pos, *w, **kw, log=False)
