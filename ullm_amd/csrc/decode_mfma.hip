@@ -95,8 +95,8 @@ __device__ void finish_unit(const float *sm_m, const float *sm_l, const float *s
 
 // PG: paged cache, addressed as in decode_dma_kernel below (a block's loads
 // go through a buffer resource based at its page).
-template <class T, int D, bool PG = false>
-__global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel(
+template <class T, int D, bool PG = false, int MW = kMW>
+__global__ __launch_bounds__(MW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
     int fetch_len, int n_head, int kv_mul, int gt, int n_units, int chunk, int splits, float qscale,
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     const int c1 = min(c0 + chunk, len);
     const int cf = fetch_len > 0 ? min(c0 + chunk, fetch_len) : c1;
 
-    __shared__ __attribute__((aligned(16))) uint16_t vt_all[kMW][kTok * VP];
+    __shared__ __attribute__((aligned(16))) uint16_t vt_all[MW][kTok * VP];
     uint16_t *vt = vt_all[wave];
 
     u32x4 qh[NS], ql[NS];  // Q^T operand (filled once the first block is in flight)
@@ -291,7 +291,7 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     // Two-stage pipeline: the next block's loads are in flight while the
     // current block computes (head_dim 256 has no registers for a second
     // stage and streams one block at a time).
-    constexpr int STEP = kMW * kTok;
+    constexpr int STEP = MW * kTok;
     int tb = c0 + wave * kTok;
     Tile A_;
     issue(A_, tb);  // first block in flight while q is prepared (past c1: zeros)
@@ -333,12 +333,24 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
     // ---- wave result: head n16, d = dt*16 + kg*4 + i ----
     l_part += __shfl_xor(l_part, 16, 64);
     l_part += __shfl_xor(l_part, 32, 64);
+    if constexpr (MW == 1) {
+        // One wave: its registers are the split's result, written without an
+        // LDS round trip (as decode_dma_kernel's one-wave path).
+        if (head_ok) {
+            const int64_t u = (int64_t)b * n_units + unit;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+                store_split<D>(oacc[dt], m_run, l_part, dt * 4 + kg, n16, b, split, splits, gt,
+                               n_head, head0, u, gt * D, out, ws_ml, ws_acc);
+        }
+        return;
+    }
 
     __syncthreads();  // all waves done with their V^T tiles: reuse the LDS
     float *sm = (float *)&vt_all[0][0];
-    float *sm_m = sm;                                 // [kMW][16]
-    float *sm_l = sm + kMW * 16;                      // [kMW][16]
-    float *sm_o = sm + 2 * kMW * 16;                  // [kMW][16][D + 4]
+    float *sm_m = sm;                                 // [MW][16]
+    float *sm_l = sm + MW * 16;                      // [MW][16]
+    float *sm_o = sm + 2 * MW * 16;                  // [MW][16][D + 4]
     if (kg == 0) { sm_m[wave * 16 + n16] = m_run; sm_l[wave * 16 + n16] = l_part; }
     // Row pitch D + 4 floats: the 16 heads of a lane group land on different
     // banks (a pitch of D would put them all on one).
@@ -347,8 +359,8 @@ __global__ __launch_bounds__(kMW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel
         *(f32x4 *)&sm_o[(wave * 16 + n16) * (D + 4) + dt * 16 + kg * 4] = oacc[dt];
     __syncthreads();
 
-    finish_unit<D>(sm_m, sm_l, sm_o, b, unit, split, splits, gt, n_units, n_head, head0, out,
-                   ws_ml, ws_acc);
+    finish_unit<D, MW>(sm_m, sm_l, sm_o, b, unit, split, splits, gt, n_units, n_head, head0,
+                       out, ws_ml, ws_acc);
 }
 
 }  // namespace ullm
@@ -801,6 +813,9 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     int chunk = (visible + splits - 1) / splits;
     chunk = (chunk + kTok - 1) / kTok * kTok;
     p.chunk = chunk;
+    // head_dim 256 with one 32-key block per split: one-wave workgroups (the
+    // other three waves of a 4-wave one would have no keys).
+    if (D > 128 && p.mw == kMW && splits > 1 && (chunk == kTok || kEnvMw == 1)) p.mw = 1;
     p.splits = (visible + chunk - 1) / chunk;
     const size_t ml = ((size_t)units * p.splits * p.gt * 2 * 4 + 255) / 256 * 256;
     const size_t ac = (size_t)units * p.splits * p.gt * D * 4;
@@ -840,9 +855,12 @@ struct MainLaunch {
 template <class T, int D>
 struct MainLaunch<T, D, false> {
     template <class... A>
-    static void run(int, dim3 g, hipStream_t st, A... a) {
+    static void run(int mw, dim3 g, hipStream_t st, A... a) {
         const int32_t *nt = nullptr;
-        hipLaunchKernelGGL((decode_mfma_kernel<T, D>), g, dim3(kMW * 64), 0, st, a..., nt, 0, 0, 0);
+        if (mw == 1)
+            hipLaunchKernelGGL((decode_mfma_kernel<T, D, false, 1>), g, dim3(64), 0, st, a..., nt, 0, 0, 0);
+        else
+            hipLaunchKernelGGL((decode_mfma_kernel<T, D>), g, dim3(kMW * 64), 0, st, a..., nt, 0, 0, 0);
     }
 };
 
@@ -954,11 +972,18 @@ static void launch_paged(const MfmaPlan &p, const float *q, const void *kp, cons
                          float *out, char *ws, hipStream_t st) {
     const dim3 g(p.splits, p.n_units, batch);
     if constexpr (D > 128) {  // register-staged kernel, 4 waves
-        hipLaunchKernelGGL((decode_mfma_kernel<T, D, true>), g, dim3(kMW * 64), 0, st, q,
-                           (const char *)kp, (const char *)vp, kvs, (int64_t)0, lens, win, 0, nh,
-                           kv_mul, p.gt, p.n_units, p.chunk, p.splits, qs, out,
-                           (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), tab, tab_stride,
-                           shift, n_pages);
+        if (p.mw == 1)
+            hipLaunchKernelGGL((decode_mfma_kernel<T, D, true, 1>), g, dim3(64), 0, st, q,
+                               (const char *)kp, (const char *)vp, kvs, (int64_t)0, lens, win, 0,
+                               nh, kv_mul, p.gt, p.n_units, p.chunk, p.splits, qs, out,
+                               (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), tab,
+                               tab_stride, shift, n_pages);
+        else
+            hipLaunchKernelGGL((decode_mfma_kernel<T, D, true>), g, dim3(kMW * 64), 0, st, q,
+                               (const char *)kp, (const char *)vp, kvs, (int64_t)0, lens, win, 0,
+                               nh, kv_mul, p.gt, p.n_units, p.chunk, p.splits, qs, out,
+                               (float *)(ws + p.off_ml), (float *)(ws + p.off_acc), tab,
+                               tab_stride, shift, n_pages);
     } else {
         auto go = [&](auto mwc) {
             constexpr int MW = decltype(mwc)::value;
