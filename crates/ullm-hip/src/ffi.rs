@@ -13,8 +13,9 @@ pub const ULLM_DT_F32: c_int = 0;
 pub const ULLM_DT_F16: c_int = 1;
 pub const ULLM_DT_BF16: c_int = 2;
 
+// `unsafe extern`: required by edition 2024 (the workspace edition).
 #[link(name = "ullm_hip")]
-extern "C" {
+unsafe extern "C" {
     pub fn ullm_hip_version() -> *const c_char;
     pub fn ullm_hip_last_error() -> *const c_char;
     /// Measurement only (no GpuForward call site): one read-only pass over

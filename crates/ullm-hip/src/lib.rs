@@ -22,7 +22,7 @@ pub mod ffi;
 mod hip {
     use std::os::raw::{c_int, c_void};
     #[link(name = "amdhip64")]
-    extern "C" {
+    unsafe extern "C" {
         pub fn hipMalloc(p: *mut *mut c_void, bytes: usize) -> c_int;
         pub fn hipFree(p: *mut c_void) -> c_int;
         pub fn hipMemset(p: *mut c_void, v: c_int, bytes: usize) -> c_int;
