@@ -115,10 +115,15 @@ size_t ullm_hip_decode_noalloc_max_bytes(void);
  * shader.metal:1051).  The cache must already hold positions
  * 0..start_pos+S-1 (lib.rs:1056-1058).
  * q:     [S][n_head*head_dim] in `dtype` (after Q-norm and RoPE)
- * cache: `dtype` (f16 or bf16; the same dtype as q)
+ * cache: `dtype` (f16, bf16 or f32; the same dtype as q)
  * out:   [S][n_head*head_dim] f32
- * head_dim in {64, 128, 256}.  For bf16, P.V runs in f16 (V is widened to
- * f16 on chip), so |V| must stay below 65504. */
+ * head_dim in {64, 128, 256}; an f32 cache (the reference's own cache dtype)
+ * takes head_dim 64 or 128 (ULLM_HIP_E_UNSUPPORTED for 256: attend row by
+ * row with ullm_hip_attn_decode, batch = S, seq_stride 0).  With an f32
+ * cache Q.K runs on bf16 hi + lo halves of Q and K (~2^-16 per product) and
+ * V is rounded to f16.  For bf16 and f32 caches P.V runs in f16 (V is
+ * converted to f16 on chip), so |V| must stay below 65504.  A layer's cache
+ * must stay below 2 GiB. */
 int ullm_hip_attn_prefill(const void *q, const void *k_cache, const void *v_cache, int dtype,
                           int64_t kv_stride, int S, int start_pos, int window, int n_head,
                           int n_kv_head, int head_dim, float scale, float *out, void *stream);

@@ -76,7 +76,10 @@ def test_decode_argument_validation():
 
 def test_prefill_and_append_validation():
     lib = L.lib()
-    assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_F32, 256, 16, 0, 0, 8, 2, 128, 0.1,
+    # f32 caches take head_dim 64/128; 256 is unsupported
+    assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_F32, 512, 16, 0, 0, 8, 2, 256, 0.1,
+                                     None, None) == L.E_UNSUPPORTED
+    assert lib.ullm_hip_attn_prefill(None, None, None, 7, 256, 16, 0, 0, 8, 2, 128, 0.1,
                                      None, None) == L.E_UNSUPPORTED
     assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_BF16, 256, 16, 0, 0, 8, 3, 128,
                                      0.1, None, None) == L.E_INVALID

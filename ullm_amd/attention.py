@@ -185,8 +185,9 @@ def attn_prefill(q, k_cache, v_cache, n_head, n_kv_head, head_dim, *, start_pos=
                  scale=None, kv_stride=None, out=None, stream=None):
     """Causal prefill attention on MFMA (lib.rs:1061-1087).
 
-    q: [S, n_head*head_dim] in the cache dtype (f16/bf16); the cache already
-    holds positions 0..start_pos+S-1.  Returns [S, n_head*head_dim] f32.
+    q: [S, n_head*head_dim] in the cache dtype (f16/bf16; or f32 with an f32
+    cache, head_dim 64/128); the cache already holds positions
+    0..start_pos+S-1.  Returns [S, n_head*head_dim] f32.
     """
     S = q.shape[0]
     _need_cuda(q, k_cache, v_cache)
@@ -387,8 +388,9 @@ class GpuAttention:
         return out.view(S, -1)
 
     def supports_batched_prefill(self) -> bool:
-        """Prefill runs on MFMA for f16/bf16 caches; an f32 cache takes the
-        split-KV kernel with one ragged sequence per query row."""
+        """Prefill runs on MFMA for every cache dtype at head_dim 64/128 (an
+        f32 cache with Q.K on bf16 hi + lo halves); an f32 cache at head_dim
+        256 takes the split-KV kernel with one ragged sequence per query row."""
         return True
 
     def _window(self, layer: int) -> int:
@@ -431,6 +433,10 @@ class GpuAttention:
         if p.kv_dtype == torch.float32:
             qr = self._append(layer, q, k, v, start_pos, torch.float32, (q_norm, k_norm),
                               (q_bias, k_bias, v_bias))
+            if p.head_dim in (64, 128):  # f32 MFMA prefill (Q.K on bf16 hi + lo)
+                return attn_prefill(qr, self.key_cache[layer], self.val_cache[layer], p.n_head,
+                                    p.n_kv_head, p.head_dim, start_pos=start_pos,
+                                    window=self._window(layer), scale=self.scale)
             return self._rows_decode(layer, qr, start_pos, S)
         qr = self._append(layer, q, k, v, start_pos, p.kv_dtype, (q_norm, k_norm),
                           (q_bias, k_bias, v_bias))
@@ -484,7 +490,7 @@ class GpuAttention:
                              rotary_dim=self.rotary_dim, neox=p.rope_neox, q_norm=q_norm,
                              k_norm=k_norm, eps=p.eps, q_bias=q_bias, k_bias=k_bias,
                              v_bias=v_bias, q_dtype=q_dtype)
-        if p.kv_dtype == torch.float32:
+        if p.kv_dtype == torch.float32 and p.head_dim not in (64, 128):
             return self._rows_decode(layer, qr, start_pos, S)
         return attn_prefill(qr, self.key_cache[layer], self.val_cache[layer], p.n_head,
                             p.n_kv_head, p.head_dim, start_pos=start_pos,

@@ -1193,6 +1193,284 @@ static int launch_prefill(const void *q, const void *kc, const void *vc, int64_t
     return check_hip(hipGetLastError(), "prefill launch");
 }
 
+// ---------------------------------------------------------------------------
+// Prefill over an f32 cache (the reference's own cache dtype,
+// crates/ullm-metal/src/forward.rs:355-356), head_dim 64 or 128.
+//
+// The matrix cores take 16-bit inputs, so Q.K runs on bf16 hi + lo halves of
+// both operands: x = hi + lo with hi = RNE(x), lo = RNE(x - hi), and
+// S = Qhi.Khi + Qhi.Klo + Qlo.Khi (three MFMAs per k-step; the dropped
+// Qlo.Klo term and the split residues are ~2^-16 of each product, far below
+// the 1e-3 budget, where plain bf16 or f16 Q/K would cost it for scores above
+// a few units).  V is rounded to f16 (2^-11, as P is), so P.V stays one f16
+// MFMA per k-step; |V| must stay below 65504.
+//
+// Layout follows prefill_sk_kernel: a workgroup owns one 32-row block of one
+// query head and its 4 waves (one per SIMD) split the block's 32-key tiles
+// into 4 contiguous ranges, merged through LDS at the end.  Per wave and
+// tile, K and V arrive as f32 in registers, a tile ahead: K is split into
+// its hi/lo operands in the MFMA A-operand layout (lane = key row), V is
+// rounded to f16 and written row-major (kv_swz swizzle) to the wave's LDS
+// tile, from which the transposing reads give the V^T operand.
+template <int D>
+__global__ __launch_bounds__(256, 1) void prefill_f32_kernel(
+    const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
+    int64_t kv_stride, int S, int start_pos, int window, int n_head, int kv_mul, int nb,
+    float qscale, float *__restrict__ out) {
+    constexpr int BN = 32, RB = D * 2;          // keys per tile; f16 LDS bytes per key row
+    constexpr int NKS = D / 16, NDT = D / 32;   // QK k-steps of 16 d; PV d tiles of 32
+    constexpr int SLOTS = D / 8;                // 16-byte (8-half) chunks per f16 row
+    constexpr int VCH = BN * SLOTS / 64;        // f16 chunks of a V tile per lane
+    constexpr int TILE = BN * RB;               // bytes of one f16 V tile
+    constexpr int PART = 32 * D * 4;            // bytes of one wave's f32 partial
+    constexpr int WREG = TILE > PART ? TILE : PART;
+    constexpr float kLazy = 8.0f;
+    static_assert(D == 64 || D == 128, "f32 prefill serves head_dim 64 and 128");
+    auto swz = [](int r) { return kv_swz<D>(r); };
+    __shared__ __attribute__((aligned(1024))) char lds[4 * WREG];
+    __shared__ float sm_ml[4][32][2];
+
+    const int total = n_head * nb;
+    const int per_xcd = (total + 7) / 8;
+    const int tsk = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (tsk >= total) return;
+    const int head = tsk / nb, blk = nb - 1 - tsk % nb;
+    const int kvh = head / kv_mul;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, h2 = lane >> 5;
+    const int q0 = blk * 32;
+    const int64_t q_dim = (int64_t)n_head * D;
+    const int kv_len = start_pos + S;
+
+    const int hi = start_pos + min(q0 + 32, S);
+    int lo = 0;
+    if (window > 0) lo = max(0, start_pos + q0 + 1 - window);
+    lo = lo / BN * BN;
+    const int nt = (hi - lo + BN - 1) / BN;
+    const int ta = lo / BN + nt * wave / 4, tb = lo / BN + nt * (wave + 1) / 4;
+
+    // Q rows of this wave (B operand, d = s*16 + h2*8 + j), split hi + lo.
+    const int qrow = q0 + c;
+    const bool row_ok = qrow < S;
+    const int pos_row = start_pos + qrow;
+    u32x4 qh[NKS], ql[NKS];
+    {
+        const float *qp = q + (int64_t)(row_ok ? qrow : 0) * q_dim + (int64_t)head * D + h2 * 8;
+#pragma unroll
+        for (int s = 0; s < NKS; s++) {
+            const f32x4 a = row_ok ? *(const f32x4 *)(qp + s * 16) : f32x4{0.f, 0.f, 0.f, 0.f};
+            const f32x4 b = row_ok ? *(const f32x4 *)(qp + s * 16 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+            const u32x2 p0 = split2<BF16>(a[0], a[1]), p1 = split2<BF16>(a[2], a[3]);
+            const u32x2 p2 = split2<BF16>(b[0], b[1]), p3 = split2<BF16>(b[2], b[3]);
+            qh[s] = u32x4{p0[0], p1[0], p2[0], p3[0]};
+            ql[s] = u32x4{p0[1], p1[1], p2[1], p3[1]};
+        }
+    }
+
+    // f32 cache rows of this kv head; loads past the range read zero.
+    const int rbg = (int)(kv_stride * 4);
+    const int range = (kv_len - 1) * rbg + D * 4;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + (int64_t)kvh * D), 0, range, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + (int64_t)kvh * D), 0, range, kRsrcWord3);
+    // Tiles past this wave's range are addressed past the buffer (zeros,
+    // no memory access), so every wave issues the same requests.
+    auto tile_off = [&](int t) { return __builtin_amdgcn_readfirstlane(t < tb ? t * BN * rbg : range); };
+    // K: lane (key c, d = s*16 + h2*8 .. +7) as two 16-byte loads per k-step.
+    const int koff = c * rbg + h2 * 32;
+    // V: lane takes f16 chunks ci = lane + 64 i of the tile: key ci / SLOTS,
+    // d = (ci % SLOTS) * 8 .. +7, as two 16-byte f32 loads.
+    u32x4 kraw[2 * NKS], vraw[2 * VCH];
+    auto issue = [&](int t) {
+        const int so = tile_off(t);
+#pragma unroll
+        for (int s = 0; s < NKS; s++)
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                kraw[2 * s + h] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff + s * 64 + h * 16 + so, 0, 0));
+#pragma unroll
+        for (int i = 0; i < VCH; i++) {
+            const int ci = lane + 64 * i, r = ci / SLOTS, p = ci % SLOTS;
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                vraw[2 * i + h] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, r * rbg + p * 32 + h * 16 + so, 0, 0));
+        }
+    };
+    char *const vt = lds + wave * WREG;  // this wave's f16 V tile
+    const uint32_t vbase = lds_addr(vt);
+
+    // V^T operand addresses (as prefill_sk_kernel): lane gets d = dt*32 + ...
+    const int g16 = lane >> 4, i16 = lane & 15;
+    uint32_t va_addr[NDT][2];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int e0 = dt * 32 + (g16 & 1) * 16 + 4 * (i16 & 3);
+            const int R = (g16 >> 1) * 4 + (i16 >> 2) + h * 8;
+            va_addr[dt][h] = vbase + R * RB + (((e0 >> 3) ^ swz(R)) * 16) + (e0 & 7) * 2;
+        }
+
+    f32x16 oacc[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
+    float m_run = -INFINITY, l_part = 0.f;
+
+    issue(ta);
+    for (int t = ta; t < tb; t++) {
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));
+        // V(t) -> f16 rows in LDS; K(t) -> hi/lo operands
+#pragma unroll
+        for (int i = 0; i < VCH; i++) {
+            const int ci = lane + 64 * i, r = ci / SLOTS, p = ci % SLOTS;
+            const f32x4 a = __builtin_bit_cast(f32x4, vraw[2 * i]);
+            const f32x4 b = __builtin_bit_cast(f32x4, vraw[2 * i + 1]);
+            lds_write_b128(vbase + r * RB + ((p ^ swz(r)) * 16),
+                           u32x4{pack_f16x2(a[0], a[1]), pack_f16x2(a[2], a[3]),
+                                 pack_f16x2(b[0], b[1]), pack_f16x2(b[2], b[3])});
+        }
+        u32x4 kh[NKS], kl[NKS];
+#pragma unroll
+        for (int s = 0; s < NKS; s++) {
+            const f32x4 a = __builtin_bit_cast(f32x4, kraw[2 * s]);
+            const f32x4 b = __builtin_bit_cast(f32x4, kraw[2 * s + 1]);
+            const u32x2 p0 = split2<BF16>(a[0], a[1]), p1 = split2<BF16>(a[2], a[3]);
+            const u32x2 p2 = split2<BF16>(b[0], b[1]), p3 = split2<BF16>(b[2], b[3]);
+            kh[s] = u32x4{p0[0], p1[0], p2[0], p3[0]};
+            kl[s] = u32x4{p0[1], p1[1], p2[1], p3[1]};
+        }
+        if (t + 1 < tb) issue(t + 1);  // raw registers consumed: next tile in flight
+        // S^T = K.Q^T in three bf16 products, two accumulation chains
+        f32x16 sa = f32x16{}, sb = f32x16{};
+#pragma unroll
+        for (int s = 0; s < NKS; s++) {
+            sa = mfma32<BF16>(kh[s], qh[s], sa);
+            sb = mfma32<BF16>(kh[s], ql[s], sb);
+            sa = mfma32<BF16>(kl[s], qh[s], sa);
+        }
+        f32x16 sacc = sa + sb;
+        const int kb = t * BN;
+        const bool need_mask = kb + BN - 1 > start_pos + q0 ||
+                               (window > 0 && kb <= start_pos + q0 + 31 - window);
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            float sv = sacc[i] * qscale;
+            if (need_mask) {
+                const int key = kb + (i >> 2) * 8 + h2 * 4 + (i & 3);
+                const bool dead = key > pos_row || (window > 0 && key <= pos_row - window);
+                sv = dead ? -INFINITY : sv;
+            }
+            sacc[i] = sv;
+            mloc = fmaxf(mloc, sv);
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        if (__any(mloc > m_run + kLazy)) {
+            const float m_new = fmaxf(m_run, mloc);
+            if (__any(m_run != -INFINITY)) {
+                const float corr = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+                l_part *= corr;
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) oacc[dt] *= corr;
+            }
+            m_run = m_new;
+        }
+        const float mu = m_run == -INFINITY ? 0.f : m_run;
+        u32x4 pk[2];
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const float p0 = __builtin_amdgcn_exp2f(sacc[ks * 8 + 2 * jj] - mu);
+                const float p1 = __builtin_amdgcn_exp2f(sacc[ks * 8 + 2 * jj + 1] - mu);
+                ls[jj] += p0 + p1;
+                pk[ks][jj] = pack_f16x2(p0, p1);
+            }
+        l_part += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+        // O^T += V^T.P^T from this wave's f16 tile (its writes retire first)
+        lds_wait_any();
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            u32x2 vb[2][2];
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                vb[ks][0] = lds_read_tr16_b64(va_addr[dt][0] + ks * 16 * RB);
+                vb[ks][1] = lds_read_tr16_b64(va_addr[dt][1] + ks * 16 * RB);
+            }
+            lds_wait_any();
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                tie(vb[ks][0]);
+                tie(vb[ks][1]);
+                oacc[dt] = mfma32<F16>(u32x4{vb[ks][0][0], vb[ks][0][1], vb[ks][1][0], vb[ks][1][1]},
+                                       pk[ks], oacc[dt]);
+            }
+        }
+        lds_order();  // the tile is rewritten by the next iteration
+    }
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));
+
+    // ---- merge the 4 partials through LDS (each wave's own region) ----
+    const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+    if (h2 == 0) { sm_ml[wave][c][0] = m_run; sm_ml[wave][c][1] = l_tot; }
+    const uint32_t pw = lds_addr(vt);
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            lds_write_b128(pw + c * D * 4 + (((dt * 8 + g * 2 + h2) ^ (c & 15)) * 16),
+                           __builtin_bit_cast(u32x4, f32x4{oacc[dt][g * 4], oacc[dt][g * 4 + 1],
+                                                           oacc[dt][g * 4 + 2], oacc[dt][g * 4 + 3]}));
+    lds_wait_any();
+    __syncthreads();
+    constexpr int CPW = D / 16, RPS = 64 / CPW;
+    const int ch = wave * CPW + lane % CPW;
+    for (int r0 = 0; r0 < 32; r0 += RPS) {
+        const int r = r0 + lane / CPW;
+        float mw[4], M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) { mw[w] = sm_ml[w][r][0]; M = fmaxf(M, mw[w]); }
+        const float mu = M == -INFINITY ? 0.f : M;
+        float L = 0.f;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        u32x4 pv[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+            pv[w] = lds_read_b128(lds_addr(lds + w * WREG) + r * D * 4 + ((ch ^ (r & 15)) * 16));
+        lds_wait_any();
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            tie(pv[w]);
+            const float a = __builtin_amdgcn_exp2f(mw[w] - mu);
+            L += sm_ml[w][r][1] * a;
+            acc += __builtin_bit_cast(f32x4, pv[w]) * a;
+        }
+        const float inv = L > 0.f ? 1.0f / L : 0.f;
+        if (q0 + r < S)
+            __builtin_nontemporal_store(acc * inv, (f32x4 *)(out + (int64_t)(q0 + r) * q_dim +
+                                                             (int64_t)head * D) + ch);
+    }
+}
+
+template <int D>
+static int launch_prefill_f32(const void *q, const void *kc, const void *vc, int64_t kvs, int S,
+                              int sp, int win, int nh, int kv_mul, float qs, float *out,
+                              hipStream_t st) {
+    const int nb = (S + 31) / 32;
+    const int total = nh * nb;
+    const int per_xcd = (total + 7) / 8;
+    hipLaunchKernelGGL((prefill_f32_kernel<D>), dim3(per_xcd * 8), dim3(256), 0, st,
+                       (const float *)q, (const float *)kc, (const float *)vc, kvs, S, sp, win,
+                       nh, kv_mul, nb, qs, out);
+    return check_hip(hipGetLastError(), "prefill (f32) launch");
+}
+
 template <class T>
 static int dispatch_prefill(int D, const void *q, const void *kc, const void *vc, int64_t kvs,
                             int S, int sp, int win, int nh, int kv_mul, float qs, float *out,
@@ -1213,15 +1491,21 @@ extern "C" int ullm_hip_attn_prefill(const void *q, const void *k_cache, const v
                                      int dtype, int64_t kv_stride, int S, int start_pos,
                                      int window, int n_head, int n_kv_head, int head_dim,
                                      float scale, float *out, void *stream) {
-    if (dtype != ULLM_DT_F16 && dtype != ULLM_DT_BF16)
-        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill: dtype %d (MFMA path takes f16/bf16)", dtype);
+    if (!dtype_ok(dtype))
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill: dtype %d", dtype);
+    if (dtype == ULLM_DT_F32 && head_dim == 256)
+        return set_error(ULLM_HIP_E_UNSUPPORTED,
+                         "prefill: an f32 cache takes head_dim 64 or 128 (256: attend row by row "
+                         "with ullm_hip_attn_decode)");
     if (n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || S < 0 || start_pos < 0)
         return set_error(ULLM_HIP_E_INVALID, "prefill: bad shape S=%d start_pos=%d heads=%d/%d", S,
                          start_pos, n_head, n_kv_head);
     if (head_dim != 64 && head_dim != 128 && head_dim != 256)
         return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill: head_dim %d not in {64,128,256}", head_dim);
-    if (kv_stride < (int64_t)n_kv_head * head_dim || (kv_stride * 2) % 16)
+    if (kv_stride < (int64_t)n_kv_head * head_dim || (kv_stride * dtype_bytes(dtype)) % 16)
         return set_error(ULLM_HIP_E_INVALID, "prefill: kv_stride must be >= n_kv_head*head_dim and 16-byte aligned");
+    if ((int64_t)(start_pos + S) * kv_stride * dtype_bytes(dtype) > 0x7fff0000LL)
+        return set_error(ULLM_HIP_E_INVALID, "prefill: a layer's cache exceeds 2 GiB");
     if (S == 0) return ULLM_HIP_OK;
     if (!q || !k_cache || !v_cache || !out)
         return set_error(ULLM_HIP_E_INVALID, "prefill: null tensor pointer");
@@ -1230,6 +1514,11 @@ extern "C" int ullm_hip_attn_prefill(const void *q, const void *k_cache, const v
     const float qs = scale * kLog2e;
     const int kv_mul = n_head / n_kv_head;
     hipStream_t st = (hipStream_t)stream;
+    if (dtype == ULLM_DT_F32) {
+        if (head_dim == 64)
+            return launch_prefill_f32<64>(q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
+        return launch_prefill_f32<128>(q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
+    }
     if (dtype == ULLM_DT_BF16)
         return dispatch_prefill<BF16>(head_dim, q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
     return dispatch_prefill<F16>(head_dim, q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
