@@ -39,7 +39,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "append", "proj",
-                                       "matmul", "paged", "cfg1", "cfg4", "copy", "floor"],
+                                       "matmul", "paged", "cfg1", "cfg4", "f32prefill", "copy",
+                                       "floor"],
                     default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     return ap.parse_args()
@@ -604,6 +605,9 @@ def main():
         res["cfg3"] = bench_prefill(torch, A, args, 2048, 32, 8, 128, torch.bfloat16, first=syn3)
         res["cfg3_paged"] = bench_prefill_paged(torch, A, args, 2048, 32, 8, 128, torch.bfloat16,
                                                 256)
+    if want("f32prefill"):
+        # The reference's own cache dtype (f32) through the MFMA prefill.
+        res["f32_prefill"] = bench_prefill(torch, A, args, 2048, 32, 8, 128, torch.float32)
     if want("cfg1"):
         res["cfg1"] = bench_decode(torch, A, args, 32, 8, 64, 512, 28, torch.float32, "cfg1")
     if want("cfg4"):
@@ -694,6 +698,15 @@ def main():
                          "ms": round(c4p["ms"], 4), "tflops": round(c4p["tflops"], 2),
                          "flop_causal": c4p["flop"],
                          "frac_mfma": round(c4p["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "f32_prefill": {"workload": "cfg3 shape (S=2048, 32/8 heads, head_dim 128) over an f32 "
+                                    "cache, the reference's own cache dtype: Q.K on bf16 hi + lo "
+                                    "halves of Q and K, P.V in f16",
+                        "kernel": "prefill_f32_kernel<128>",
+                        "ms": round(res["f32_prefill"]["ms"], 4),
+                        "tflops": round(res["f32_prefill"]["tflops"], 2),
+                        "frac_mfma": round(res["f32_prefill"]["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+                        "note": "the matrix cores execute 2x the algorithmic FLOP (three bf16 "
+                                "products for Q.K)"},
         "long_decode": {"workload": "cfg5 Qwen3-30B-A3B-shaped decode, 32/4 heads, head_dim "
                                     "128, bf16 KV 32768, 48 layers",
                         "us_per_layer": round(lc["us_per_layer"], 3),

@@ -255,8 +255,10 @@ impl HipAttention {
     /// lib.rs:1021-1087).  Returns [s][n_head*D] f32.
     ///  * f16/bf16 cache: q goes out in the cache dtype, then one causal
     ///    prefill launch on the matrix cores.
-    ///  * f32 cache (the reference's own): the s query rows attend as s
-    ///    ragged "sequences" over the shared cache (seq_stride 0) with lengths
+    ///  * f32 cache (the reference's own), head_dim 64/128: q stays f32 and
+    ///    the f32 prefill kernel runs Q.K on bf16 hi + lo halves.
+    ///  * f32 cache, head_dim 256: the s query rows attend as s ragged
+    ///    "sequences" over the shared cache (seq_stride 0) with lengths
     ///    1..=s, on the split-KV decode kernel.
     pub fn forward_batch(&self, layer: usize, qs: &[f32], ks: &[f32], vs: &[f32], s: usize,
                          hp: HeadParams) -> Result<Vec<f32>> {
@@ -268,7 +270,8 @@ impl HipAttention {
         self.kv.upload(ks, 0)?;
         self.kv.upload(vs, s * kd * 4)?;
         let off = self.layer_off(layer);
-        if p.kv_dtype == ffi::ULLM_DT_F32 {
+        let f32_rows = p.kv_dtype == ffi::ULLM_DT_F32 && p.head_dim == 256;
+        if f32_rows {
             self.append(layer, s, 0, hp, self.q.ptr, ffi::ULLM_DT_F32)?;
             let need = unsafe {
                 ffi::ullm_hip_decode_workspace_bytes(s as c_int, p.n_head as c_int,
@@ -289,19 +292,24 @@ impl HipAttention {
                     std::ptr::null_mut())
             })?;
         } else {
-            // q in the cache dtype into `kv`'s front half is not big enough for
-            // q_dim > 2*kv_dim, so it goes to `out` and attention writes `q`.
-            self.append(layer, s, 0, hp, self.out.ptr, p.kv_dtype)?;
+            // 16-bit caches: q in the cache dtype goes to `out` and the
+            // attention writes its f32 rows to `q`.  An f32 cache: q is
+            // prepared in place in `q` and the attention writes `out`.
+            let q_prep = if p.kv_dtype == ffi::ULLM_DT_F32 { self.q.ptr } else { self.out.ptr };
+            let o_dst = if p.kv_dtype == ffi::ULLM_DT_F32 { self.out.ptr } else { self.q.ptr };
+            self.append(layer, s, 0, hp, q_prep, p.kv_dtype)?;
             ffi::check(unsafe {
                 ffi::ullm_hip_attn_prefill(
-                    self.out.ptr, self.key_cache.at(off), self.val_cache.at(off), p.kv_dtype,
+                    q_prep, self.key_cache.at(off), self.val_cache.at(off), p.kv_dtype,
                     kd as i64, s as c_int, 0, self.window(layer), p.n_head as c_int,
-                    p.n_kv_head as c_int, p.head_dim as c_int, self.scale(), self.q.ptr.cast(),
+                    p.n_kv_head as c_int, p.head_dim as c_int, self.scale(), o_dst.cast(),
                     std::ptr::null_mut())
             })?;
-            let mut o = vec![0f32; s * p.n_head * p.head_dim];
-            self.q.download(&mut o)?;
-            return Ok(o);
+            if p.kv_dtype != ffi::ULLM_DT_F32 {
+                let mut o = vec![0f32; s * p.n_head * p.head_dim];
+                self.q.download(&mut o)?;
+                return Ok(o);
+            }
         }
         let mut o = vec![0f32; s * p.n_head * p.head_dim];
         self.out.download(&mut o)?;
