@@ -102,6 +102,9 @@ __device__ __forceinline__ u32x4 lds_read_b128(uint32_t a) {
 __device__ __forceinline__ void lds_write_b128(uint32_t a, const u32x4 &v) {
     asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
 }
+__device__ __forceinline__ void lds_write_b64(uint32_t a, const u32x2 &v) {
+    asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
 __device__ __forceinline__ u32x2 lds_read_tr16_b64(uint32_t a) {
     u32x2 r;
     asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));

@@ -1205,106 +1205,128 @@ static int launch_prefill(const void *q, const void *kc, const void *vc, int64_t
 // a few units).  V is rounded to f16 (2^-11, as P is), so P.V stays one f16
 // MFMA per k-step; |V| must stay below 65504.
 //
-// Layout follows prefill_sk_kernel: a workgroup owns one 32-row block of one
-// query head and its 4 waves (one per SIMD) split the block's 32-key tiles
-// into 4 contiguous ranges, merged through LDS at the end.  Per wave and
-// tile, K and V arrive as f32 in registers, a tile ahead: K is split into
-// its hi/lo operands in the MFMA A-operand layout (lane = key row), V is
-// rounded to f16 and written row-major (kv_swz swizzle) to the wave's LDS
-// tile, from which the transposing reads give the V^T operand.
-template <int D>
+// Q is scaled by scale*log2(e) before its split, so the scores come out in
+// the exp2 domain.
+//
+// The K/V tiles are shared by a workgroup's 4 waves.  A workgroup owns hw
+// query heads of one kv head (hw = the largest power of two dividing kv_mul,
+// at most 4) times 4/hw consecutive 32-row blocks: one "unit" of
+// UR = 128/hw rows; wave w takes head hw0 + w % hw and rows (w / hw) * 32 ..
+// +31 of the unit.  Units are taken in causal pairs, A = p and B = NU-1-p,
+// so every workgroup attends about the same number of keys.  The workgroup
+// walks the key tiles of A, then those of B, and each tile is loaded and
+// converted once for all 4 waves:
+//  * all 256 threads load the tile's f32 K and V rows (16-byte chunks, two
+//    full rows per wave instruction) into registers, NRAW tiles ahead;
+//  * they convert them into an LDS stage, a chunk at a time between the
+//    k-steps of the previous tile's Q.K (the conversion's VALU work issues
+//    while the MFMAs run): K as bf16 hi and lo rows (row pitch D*2 + 16
+//    bytes, so the 16 rows one A-operand read touches lie on distinct
+//    banks), V as f16 rows in the kv_swz layout the transposing reads expect;
+//  * three stages: a stage is rewritten two tiles after it was read, so one
+//    barrier per tile orders every rewrite after all reads of it.
+// Each wave keeps (m, l, O) of its 32 rows over the whole key range, so it
+// writes its rows of A (normalised) when A's tiles end and starts B afresh;
+// no partials are merged.  A 32-row block of one head per workgroup with the
+// 4 waves splitting its keys (each wave streaming and converting its own
+// tiles) took 1.6x as long at the cfg3 shape.
+template <int D, int NRAW = 2>
 __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
-    int64_t kv_stride, int S, int start_pos, int window, int n_head, int kv_mul, int nb,
-    float qscale, float *__restrict__ out) {
-    constexpr int BN = 32, RB = D * 2;          // keys per tile; f16 LDS bytes per key row
-    constexpr int NKS = D / 16, NDT = D / 32;   // QK k-steps of 16 d; PV d tiles of 32
-    constexpr int SLOTS = D / 8;                // 16-byte (8-half) chunks per f16 row
-    constexpr int VCH = BN * SLOTS / 64;        // f16 chunks of a V tile per lane
-    constexpr int TILE = BN * RB;               // bytes of one f16 V tile
-    constexpr int PART = 32 * D * 4;            // bytes of one wave's f32 partial
-    constexpr int WREG = TILE > PART ? TILE : PART;
+    int64_t kv_stride, int S, int start_pos, int window, int n_head, int kv_mul, int hw,
+    int n_units, int n_pairs, float qscale, float *__restrict__ out) {
+    constexpr int BN = 32, RB = D * 2, KP = D * 2 + 16;  // keys per tile; f16/bf16 row bytes; K pitch
+    constexpr int NKS = D / 16, NDT = D / 32;
+    constexpr int FPR = D / 4;              // 16-byte f32 chunks per cache row
+    constexpr int NCH = BN * FPR / 256;     // chunks per thread per tile (K and V each)
+    constexpr int KARR = BN * KP, VARR = BN * RB;
+    constexpr int STAGE = 2 * KARR + VARR;  // K hi, K lo, V (f16)
+    constexpr int NSTG = 3;
     constexpr float kLazy = 8.0f;
     static_assert(D == 64 || D == 128, "f32 prefill serves head_dim 64 and 128");
     auto swz = [](int r) { return kv_swz<D>(r); };
-    __shared__ __attribute__((aligned(1024))) char lds[4 * WREG];
-    __shared__ float sm_ml[4][32][2];
-
-    const int total = n_head * nb;
-    const int per_xcd = (total + 7) / 8;
-    const int tsk = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (tsk >= total) return;
-    const int head = tsk / nb, blk = nb - 1 - tsk % nb;
-    const int kvh = head / kv_mul;
+    constexpr int QB = 2 * NKS * 64 * 16;   // one wave's unit-B Q operands (hi, lo)
+    __shared__ __attribute__((aligned(1024))) char lds[NSTG * STAGE];
+    __shared__ __attribute__((aligned(16))) char qb_lds[4 * QB];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 31, h2 = lane >> 5;
-    const int q0 = blk * 32;
+    // Task: (head group, pair), pairs of one head group on one XCD's L2.
+    const int n_hg = n_head / hw;
+    const int total = n_hg * n_pairs;
+    const int per_xcd = (total + 7) / 8;
+    const int tsk = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (tsk >= total) return;
+    const int hg = tsk / n_pairs, pr = tsk % n_pairs;
+    const int rbw = 4 / hw, UR = 32 * rbw;
+    const int head = hg * hw + wave % hw, kvh = head / kv_mul;
+    const int roff = (wave / hw) * 32;  // this wave's rows within a unit
     const int64_t q_dim = (int64_t)n_head * D;
     const int kv_len = start_pos + S;
+    const int ua = pr, ub = n_units - 1 - pr;  // ub == ua: the middle unit alone
 
-    const int hi = start_pos + min(q0 + 32, S);
-    int lo = 0;
-    if (window > 0) lo = max(0, start_pos + q0 + 1 - window);
-    lo = lo / BN * BN;
-    const int nt = (hi - lo + BN - 1) / BN;
-    const int ta = lo / BN + nt * wave / 4, tb = lo / BN + nt * (wave + 1) / 4;
+    // Key tiles [first, end) of a unit: from the window start of its first
+    // row to the causal end of its last row.
+    auto tiles = [&](int u, int &t0, int &t1) {
+        const int r0 = u * UR;
+        const int hi = start_pos + min(r0 + UR, S);
+        int lo = 0;
+        if (window > 0) lo = max(0, start_pos + r0 + 1 - window);
+        t0 = lo / BN;
+        t1 = (hi + BN - 1) / BN;
+    };
+    int a0, a1, b0 = 0, b1 = 0;
+    tiles(ua, a0, a1);
+    if (ub != ua) tiles(ub, b0, b1);
+    const int na = a1 - a0, nsteps = na + (b1 - b0);
 
-    // Q rows of this wave (B operand, d = s*16 + h2*8 + j), split hi + lo.
-    const int qrow = q0 + c;
-    const bool row_ok = qrow < S;
-    const int pos_row = start_pos + qrow;
-    u32x4 qh[NKS], ql[NKS];
-    {
-        const float *qp = q + (int64_t)(row_ok ? qrow : 0) * q_dim + (int64_t)head * D + h2 * 8;
-#pragma unroll
-        for (int s = 0; s < NKS; s++) {
-            const f32x4 a = row_ok ? *(const f32x4 *)(qp + s * 16) : f32x4{0.f, 0.f, 0.f, 0.f};
-            const f32x4 b = row_ok ? *(const f32x4 *)(qp + s * 16 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
-            const u32x2 p0 = split2<BF16>(a[0], a[1]), p1 = split2<BF16>(a[2], a[3]);
-            const u32x2 p2 = split2<BF16>(b[0], b[1]), p3 = split2<BF16>(b[2], b[3]);
-            qh[s] = u32x4{p0[0], p1[0], p2[0], p3[0]};
-            ql[s] = u32x4{p0[1], p1[1], p2[1], p3[1]};
-        }
-    }
-
-    // f32 cache rows of this kv head; loads past the range read zero.
     const int rbg = (int)(kv_stride * 4);
     const int range = (kv_len - 1) * rbg + D * 4;
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + (int64_t)kvh * D), 0, range, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t vrs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + (int64_t)kvh * D), 0, range, kRsrcWord3);
-    // Tiles past this wave's range are addressed past the buffer (zeros,
-    // no memory access), so every wave issues the same requests.
-    auto tile_off = [&](int t) { return __builtin_amdgcn_readfirstlane(t < tb ? t * BN * rbg : range); };
-    // K: lane (key c, d = s*16 + h2*8 .. +7) as two 16-byte loads per k-step.
-    const int koff = c * rbg + h2 * 32;
-    // V: lane takes f16 chunks ci = lane + 64 i of the tile: key ci / SLOTS,
-    // d = (ci % SLOTS) * 8 .. +7, as two 16-byte f32 loads.
-    u32x4 kraw[2 * NKS], vraw[2 * VCH];
-    auto issue = [&](int t) {
-        const int so = tile_off(t);
+    // Step j's tile; steps past the end address past the buffer (zeros,
+    // no memory access), so every step issues the same requests.
+    auto tile_of = [&](int j) { return j < na ? a0 + j : b0 + (j - na); };
+    auto step_off = [&](int j) {
+        return __builtin_amdgcn_readfirstlane(j < nsteps ? tile_of(j) * BN * rbg : range);
+    };
+    // Thread tid loads chunks ci = tid + 256 i: row ci / FPR, f32 chunk ci % FPR.
+    u32x4 kraw[NRAW][NCH], vraw[NRAW][NCH];
+    auto issue = [&](u32x4(&kr)[NCH], u32x4(&vr)[NCH], int j) {
+        const int so = step_off(j);
 #pragma unroll
-        for (int s = 0; s < NKS; s++)
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-                kraw[2 * s + h] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff + s * 64 + h * 16 + so, 0, 0));
-#pragma unroll
-        for (int i = 0; i < VCH; i++) {
-            const int ci = lane + 64 * i, r = ci / SLOTS, p = ci % SLOTS;
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-                vraw[2 * i + h] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, r * rbg + p * 32 + h * 16 + so, 0, 0));
+        for (int i = 0; i < NCH; i++) {
+            const int ci = tid + 256 * i, off = (ci / FPR) * rbg + (ci % FPR) * 16 + so;
+            kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
+            vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
         }
     };
-    char *const vt = lds + wave * WREG;  // this wave's f16 V tile
-    const uint32_t vbase = lds_addr(vt);
+    const uint32_t lds0 = lds_addr(lds);
+    // Chunk i of the thread's share (one K and one V chunk).
+    auto convert1 = [&](const u32x4(&kr)[NCH], const u32x4(&vr)[NCH], int stg, int i) {
+        const uint32_t sb = lds0 + stg * STAGE;
+        {
+            const int ci = tid + 256 * i, r = ci / FPR, f = ci % FPR;
+            const f32x4 kv = __builtin_bit_cast(f32x4, kr[i]);
+            const u32x2 p0 = split2<BF16>(kv[0], kv[1]), p1 = split2<BF16>(kv[2], kv[3]);
+            lds_write_b64(sb + r * KP + f * 8, u32x2{p0[0], p1[0]});
+            lds_write_b64(sb + KARR + r * KP + f * 8, u32x2{p0[1], p1[1]});
+            const f32x4 vv = __builtin_bit_cast(f32x4, vr[i]);
+            lds_write_b64(sb + 2 * KARR + r * RB + (((f >> 1) ^ swz(r)) * 16) + (f & 1) * 8,
+                          u32x2{pack_f16x2(vv[0], vv[1]), pack_f16x2(vv[2], vv[3])});
+        }
+    };
+    auto convert = [&](const u32x4(&kr)[NCH], const u32x4(&vr)[NCH], int stg) {
+#pragma unroll
+        for (int i = 0; i < NCH; i++) convert1(kr, vr, stg, i);
+    };
 
-    // V^T operand addresses (as prefill_sk_kernel): lane gets d = dt*32 + ...
+    // Operand addresses within a stage: K (lane = key c, d = s*16 + h2*8 ..),
+    // V^T (as prefill_sk_kernel).
+    const uint32_t ka = c * KP + h2 * 16;
     const int g16 = lane >> 4, i16 = lane & 15;
     uint32_t va_addr[NDT][2];
 #pragma unroll
@@ -1313,63 +1335,111 @@ __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(
         for (int h = 0; h < 2; h++) {
             const int e0 = dt * 32 + (g16 & 1) * 16 + 4 * (i16 & 3);
             const int R = (g16 >> 1) * 4 + (i16 >> 2) + h * 8;
-            va_addr[dt][h] = vbase + R * RB + (((e0 >> 3) ^ swz(R)) * 16) + (e0 & 7) * 2;
+            va_addr[dt][h] = 2 * KARR + R * RB + (((e0 >> 3) ^ swz(R)) * 16) + (e0 & 7) * 2;
         }
 
-    f32x16 oacc[NDT];
-#pragma unroll
-    for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
-    float m_run = -INFINITY, l_part = 0.f;
-
-    issue(ta);
-    for (int t = ta; t < tb; t++) {
-        __builtin_amdgcn_s_waitcnt(vm_wait(0));
-        // V(t) -> f16 rows in LDS; K(t) -> hi/lo operands
-#pragma unroll
-        for (int i = 0; i < VCH; i++) {
-            const int ci = lane + 64 * i, r = ci / SLOTS, p = ci % SLOTS;
-            const f32x4 a = __builtin_bit_cast(f32x4, vraw[2 * i]);
-            const f32x4 b = __builtin_bit_cast(f32x4, vraw[2 * i + 1]);
-            lds_write_b128(vbase + r * RB + ((p ^ swz(r)) * 16),
-                           u32x4{pack_f16x2(a[0], a[1]), pack_f16x2(a[2], a[3]),
-                                 pack_f16x2(b[0], b[1]), pack_f16x2(b[2], b[3])});
-        }
-        u32x4 kh[NKS], kl[NKS];
+    // Per-unit state of this wave: Q as hi/lo B operands (unit B's are
+    // prepared at the start and parked in LDS, lane-major), row, (m, l, O).
+    u32x4 qh[NKS], ql[NKS];
+    const uint32_t qbw = lds_addr(qb_lds) + wave * QB + lane * 16;
+    auto load_q = [&](int u, u32x4(&h)[NKS], u32x4(&l)[NKS]) {
+        const int row = u * UR + roff + c;
+        const bool ok = row < S;
+        const float *qp = q + (int64_t)(ok ? row : 0) * q_dim + (int64_t)head * D + h2 * 8;
 #pragma unroll
         for (int s = 0; s < NKS; s++) {
-            const f32x4 a = __builtin_bit_cast(f32x4, kraw[2 * s]);
-            const f32x4 b = __builtin_bit_cast(f32x4, kraw[2 * s + 1]);
+            // scaled before the split: the scores come out in the exp2 domain
+            const f32x4 a = (ok ? *(const f32x4 *)(qp + s * 16) : f32x4{0.f, 0.f, 0.f, 0.f}) * qscale;
+            const f32x4 b = (ok ? *(const f32x4 *)(qp + s * 16 + 4) : f32x4{0.f, 0.f, 0.f, 0.f}) * qscale;
             const u32x2 p0 = split2<BF16>(a[0], a[1]), p1 = split2<BF16>(a[2], a[3]);
             const u32x2 p2 = split2<BF16>(b[0], b[1]), p3 = split2<BF16>(b[2], b[3]);
-            kh[s] = u32x4{p0[0], p1[0], p2[0], p3[0]};
-            kl[s] = u32x4{p0[1], p1[1], p2[1], p3[1]};
+            h[s] = u32x4{p0[0], p1[0], p2[0], p3[0]};
+            l[s] = u32x4{p0[1], p1[1], p2[1], p3[1]};
         }
-        if (t + 1 < tb) issue(t + 1);  // raw registers consumed: next tile in flight
-        // S^T = K.Q^T in three bf16 products, two accumulation chains
-        f32x16 sa = f32x16{}, sb = f32x16{};
+    };
+    int qrow = 0, pos_row = 0;
+    const int dlo = window > 0 ? -window : INT_MIN;
+    f32x16 oacc[NDT];
+    float m_run, l_part;
+    auto begin_unit = [&](int u) {
+        qrow = u * UR + roff + c;
+        pos_row = start_pos + qrow;
+#pragma unroll
+        for (int i = 0; i < NDT; i++) oacc[i] = f32x16{};
+        m_run = -INFINITY;
+        l_part = 0.f;
+    };
+    // O^T in registers: lane (row c, h2) holds d = dt*32 + 8g + 4*h2 + 0..3.
+    auto end_unit = [&]() {
+        const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+        const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+        if (qrow < S) {
+            float *op = out + (int64_t)qrow * q_dim + (int64_t)head * D + h2 * 4;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    __builtin_nontemporal_store(
+                        f32x4{oacc[dt][g * 4], oacc[dt][g * 4 + 1], oacc[dt][g * 4 + 2],
+                              oacc[dt][g * 4 + 3]} * inv,
+                        (f32x4 *)(op + dt * 32 + g * 8));
+        }
+    };
+
+    // mid(i) runs after k-step 2i+1 of Q.K (the next tile's conversion, one
+    // chunk at a time, so its VALU work issues while the MFMAs run).
+    auto compute = [&](int j, int stg, auto &&mid) {
+        const uint32_t sb = lds0 + stg * STAGE;
+        f32x16 sacc = f32x16{};
+        // K operands of k-step s+1 are read while s's MFMAs run.
+        u32x4 kh[2], kl[2];
+        kh[0] = lds_read_b128(sb + ka);
+        kl[0] = lds_read_b128(sb + KARR + ka);
 #pragma unroll
         for (int s = 0; s < NKS; s++) {
-            sa = mfma32<BF16>(kh[s], qh[s], sa);
-            sb = mfma32<BF16>(kh[s], ql[s], sb);
-            sa = mfma32<BF16>(kl[s], qh[s], sa);
-        }
-        f32x16 sacc = sa + sb;
-        const int kb = t * BN;
-        const bool need_mask = kb + BN - 1 > start_pos + q0 ||
-                               (window > 0 && kb <= start_pos + q0 + 31 - window);
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            float sv = sacc[i] * qscale;
-            if (need_mask) {
-                const int key = kb + (i >> 2) * 8 + h2 * 4 + (i & 3);
-                const bool dead = key > pos_row || (window > 0 && key <= pos_row - window);
-                sv = dead ? -INFINITY : sv;
+            if (s + 1 < NKS) {
+                kh[(s + 1) & 1] = lds_read_b128(sb + ka + (s + 1) * 32);
+                kl[(s + 1) & 1] = lds_read_b128(sb + KARR + ka + (s + 1) * 32);
+                asm volatile("s_waitcnt lgkmcnt(2)" ::: "memory");
+            } else {
+                lds_wait_any();
             }
-            sacc[i] = sv;
-            mloc = fmaxf(mloc, sv);
+            tie(kh[s & 1]);
+            tie(kl[s & 1]);
+            sacc = mfma32<BF16>(kh[s & 1], qh[s], sacc);
+            sacc = mfma32<BF16>(kh[s & 1], ql[s], sacc);
+            sacc = mfma32<BF16>(kl[s & 1], qh[s], sacc);
+            if (s & 1) mid(s >> 1);
         }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        // V^T operands of d tile 0 go out before the softmax
+        u32x2 vb[2][2][2];
+        auto rd = [&](int dt, int buf) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                vb[buf][ks][0] = lds_read_tr16_b64(sb + va_addr[dt][0] + ks * 16 * RB);
+                vb[buf][ks][1] = lds_read_tr16_b64(sb + va_addr[dt][1] + ks * 16 * RB);
+            }
+        };
+        rd(0, 0);
+        // Masked only where the tile reaches past the diagonal of the
+        // wave's first row or before the window of its last (wave-uniform):
+        // key - pos_row must lie in (dlo, 0].
+        const int kb = tile_of(j) * BN, p_first = pos_row - c;
+        float mloc = -INFINITY;
+        if (kb + BN - 1 > p_first || (window > 0 && kb <= p_first + 31 - window)) {
+            const int kd = kb + h2 * 4 - pos_row;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int dk = kd + (i >> 2) * 8 + (i & 3);
+                const float sv = dk > 0 || dk <= dlo ? -INFINITY : sacc[i];
+                sacc[i] = sv;
+                mloc = fmaxf(mloc, sv);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) mloc = fmaxf(mloc, sacc[i]);
+        }
+        mloc = max_xor32(mloc);
         if (__any(mloc > m_run + kLazy)) {
             const float m_new = fmaxf(m_run, mloc);
             if (__any(m_run != -INFINITY)) {
@@ -1393,81 +1463,97 @@ __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(
                 pk[ks][jj] = pack_f16x2(p0, p1);
             }
         l_part += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-        // O^T += V^T.P^T from this wave's f16 tile (its writes retire first)
-        lds_wait_any();
+        // O^T += V^T.P^T, the reads of d tile dt+1 in flight during dt's MFMAs
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
-            u32x2 vb[2][2];
+            if (dt + 1 < NDT) {
+                rd(dt + 1, (dt + 1) & 1);
+                asm volatile("s_waitcnt lgkmcnt(4)" ::: "memory");
+            } else {
+                lds_wait_any();
+            }
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) {
-                vb[ks][0] = lds_read_tr16_b64(va_addr[dt][0] + ks * 16 * RB);
-                vb[ks][1] = lds_read_tr16_b64(va_addr[dt][1] + ks * 16 * RB);
+                tie(vb[dt & 1][ks][0]);
+                tie(vb[dt & 1][ks][1]);
+                const u32x2 a0 = vb[dt & 1][ks][0], a1 = vb[dt & 1][ks][1];
+                oacc[dt] = mfma32<F16>(u32x4{a0[0], a0[1], a1[0], a1[1]}, pk[ks], oacc[dt]);
+            }
+        }
+    };
+
+    // ---- pipeline: raw tiles NRAW ahead in registers, 3 converted stages ----
+    static_assert(NRAW == 2, "the step loop is unrolled for two raw register sets");
+    issue(kraw[0], vraw[0], 0);
+    issue(kraw[1], vraw[1], 1);
+    if (ub != ua) {
+        load_q(ub, qh, ql);
+#pragma unroll
+        for (int s = 0; s < NKS; s++) {
+            lds_write_b128(qbw + (2 * s) * 1024, qh[s]);
+            lds_write_b128(qbw + (2 * s + 1) * 1024, ql[s]);
+        }
+    }
+    load_q(ua, qh, ql);
+    begin_unit(ua);
+    convert(kraw[0], vraw[0], 0);
+    issue(kraw[0], vraw[0], 2);
+    lds_wait_any();
+    __syncthreads();
+    // Step j: compute tile j from stage j%3 while converting tile j+1 (raw
+    // set (j+1)%2) into stage (j+1)%3, request tile j+3 into that set, then
+    // a barrier: tile j+1's stage is complete for every wave, and stage
+    // (j+2)%3, read by compute(j-1), is free for the next conversion.
+    int stg = 0;
+    auto step = [&](auto rs, int j, bool live) {
+        constexpr int R = decltype(rs)::value;  // raw set of tile j+1
+        const int nstg = stg == NSTG - 1 ? 0 : stg + 1;
+        if (live && j == na) {
+            end_unit();
+            begin_unit(ub);
+#pragma unroll
+            for (int s = 0; s < NKS; s++) {
+                qh[s] = lds_read_b128(qbw + (2 * s) * 1024);
+                ql[s] = lds_read_b128(qbw + (2 * s + 1) * 1024);
             }
             lds_wait_any();
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                tie(vb[ks][0]);
-                tie(vb[ks][1]);
-                oacc[dt] = mfma32<F16>(u32x4{vb[ks][0][0], vb[ks][0][1], vb[ks][1][0], vb[ks][1][1]},
-                                       pk[ks], oacc[dt]);
-            }
+            for (int s = 0; s < NKS; s++) { tie(qh[s]); tie(ql[s]); }
         }
-        lds_order();  // the tile is rewritten by the next iteration
-    }
-    __builtin_amdgcn_s_waitcnt(vm_wait(0));
-
-    // ---- merge the 4 partials through LDS (each wave's own region) ----
-    const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
-    if (h2 == 0) { sm_ml[wave][c][0] = m_run; sm_ml[wave][c][1] = l_tot; }
-    const uint32_t pw = lds_addr(vt);
-#pragma unroll
-    for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-            lds_write_b128(pw + c * D * 4 + (((dt * 8 + g * 2 + h2) ^ (c & 15)) * 16),
-                           __builtin_bit_cast(u32x4, f32x4{oacc[dt][g * 4], oacc[dt][g * 4 + 1],
-                                                           oacc[dt][g * 4 + 2], oacc[dt][g * 4 + 3]}));
-    lds_wait_any();
-    __syncthreads();
-    constexpr int CPW = D / 16, RPS = 64 / CPW;
-    const int ch = wave * CPW + lane % CPW;
-    for (int r0 = 0; r0 < 32; r0 += RPS) {
-        const int r = r0 + lane / CPW;
-        float mw[4], M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < 4; w++) { mw[w] = sm_ml[w][r][0]; M = fmaxf(M, mw[w]); }
-        const float mu = M == -INFINITY ? 0.f : M;
-        float L = 0.f;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        u32x4 pv[4];
-#pragma unroll
-        for (int w = 0; w < 4; w++)
-            pv[w] = lds_read_b128(lds_addr(lds + w * WREG) + r * D * 4 + ((ch ^ (r & 15)) * 16));
+        if (live) compute(j, stg, [&](int i) { convert1(kraw[R], vraw[R], nstg, i); });
+        else convert(kraw[R], vraw[R], nstg);
+        issue(kraw[R], vraw[R], j + 3);
+        // LDS writes done, then a barrier that leaves the tile requests in
+        // flight (a fence would wait for them); the clobber keeps LDS
+        // accesses on their side of it.
         lds_wait_any();
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            tie(pv[w]);
-            const float a = __builtin_amdgcn_exp2f(mw[w] - mu);
-            L += sm_ml[w][r][1] * a;
-            acc += __builtin_bit_cast(f32x4, pv[w]) * a;
-        }
-        const float inv = L > 0.f ? 1.0f / L : 0.f;
-        if (q0 + r < S)
-            __builtin_nontemporal_store(acc * inv, (f32x4 *)(out + (int64_t)(q0 + r) * q_dim +
-                                                             (int64_t)head * D) + ch);
+        asm volatile("s_barrier" ::: "memory");
+        stg = nstg;
+    };
+    // Both halves convert, request and synchronise unconditionally (a path
+    // that skipped the second half's requests would make every wait at the
+    // loop head drain all of them); only the compute of a step past the end
+    // is skipped.
+    for (int j = 0; j < nsteps; j += 2) {
+        step(Int<1>{}, j, true);
+        step(Int<0>{}, j + 1, j + 1 < nsteps);
     }
+    end_unit();
 }
 
 template <int D>
 static int launch_prefill_f32(const void *q, const void *kc, const void *vc, int64_t kvs, int S,
                               int sp, int win, int nh, int kv_mul, float qs, float *out,
                               hipStream_t st) {
-    const int nb = (S + 31) / 32;
-    const int total = nh * nb;
+    int hw = 1;
+    while (hw < 4 && kv_mul % (hw * 2) == 0) hw *= 2;
+    const int n_units = (S + 128 / hw - 1) / (128 / hw);
+    const int n_pairs = (n_units + 1) / 2;
+    const int total = nh / hw * n_pairs;
     const int per_xcd = (total + 7) / 8;
     hipLaunchKernelGGL((prefill_f32_kernel<D>), dim3(per_xcd * 8), dim3(256), 0, st,
                        (const float *)q, (const float *)kc, (const float *)vc, kvs, S, sp, win,
-                       nh, kv_mul, nb, qs, out);
+                       nh, kv_mul, hw, n_units, n_pairs, qs, out);
     return check_hip(hipGetLastError(), "prefill (f32) launch");
 }
 
