@@ -904,6 +904,7 @@ __global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
     const int qrow = q0 + c;
     const bool row_ok = qrow < S;
     const int pos_row = start_pos + qrow;
+    const int dlo = window > 0 ? -window : INT_MIN;
     u32x4 qreg[NKS];
     {
         const uint16_t *qp = q + (int64_t)(row_ok ? qrow : 0) * q_dim + (int64_t)head * D + h2 * 8;
@@ -999,18 +1000,14 @@ __global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
 #pragma unroll
         for (int s = 0; s < NKS; s++) sacc = mfma32<T>(kreg[s], qreg[s], sacc);
         issue_k(kreg, t + 1);  // the MFMAs above have read their K
-        const int kb = t * BN;
-        const bool need_mask = kb + BN - 1 > start_pos + q0 ||
-                               (window > 0 && kb <= start_pos + q0 + 31 - window);
+        // Masked without branches: key - pos_row = kd + (i>>2)*8 + (i&3) must
+        // lie in (dlo, 0] (dlo = -window, or below any offset with no window).
+        const int kd = t * BN + h2 * 4 - pos_row;
         float mloc = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            float sv = sacc[i] * qscale;
-            if (need_mask) {
-                const int key = kb + (i >> 2) * 8 + h2 * 4 + (i & 3);
-                const bool dead = key > pos_row || (window > 0 && key <= pos_row - window);
-                sv = dead ? -INFINITY : sv;
-            }
+            const int dk = kd + (i >> 2) * 8 + (i & 3);
+            const float sv = dk > 0 || dk <= dlo ? -INFINITY : sacc[i] * qscale;
             sacc[i] = sv;
             mloc = fmaxf(mloc, sv);
         }
@@ -1023,6 +1020,10 @@ __global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
             if (__any(m_run != -INFINITY)) {
                 const float corr = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
                 l_part *= corr;
+                // (pinned here, so the copies out of the accumulation
+                // registers stay inside this rare branch)
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) asm volatile("" : "+a"(oacc[dt]));
 #pragma unroll
                 for (int dt = 0; dt < NDT; dt++) oacc[dt] *= corr;
             }
@@ -1106,28 +1107,37 @@ __global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
                                                            oacc[dt][g * 4 + 2], oacc[dt][g * 4 + 3]}));
     __builtin_amdgcn_s_waitcnt(vm_wait(63) & ~(15 << 8));
     __syncthreads();
-    // Wave w writes chunks [w*CPW, (w+1)*CPW) of every row, 64/CPW rows at a time.
-    constexpr int RPS = 64 / CPW;
+    // Wave w writes chunks [w*CPW, (w+1)*CPW) of every row, 64/CPW rows at a
+    // time; every LDS read of the pass is issued before any is consumed.
+    constexpr int RPS = 64 / CPW, NR = 32 / RPS;
     const int ch = wave * CPW + lane % CPW;
-    for (int r0 = 0; r0 < 32; r0 += RPS) {
-        const int r = r0 + lane / CPW;
-        float mw[4], M = -INFINITY;
+    u32x4 pv[NR][4];
+    float2 ml[NR][4];
 #pragma unroll
-        for (int w = 0; w < 4; w++) { mw[w] = sm_ml[w][r][0]; M = fmaxf(M, mw[w]); }
+    for (int it = 0; it < NR; it++) {
+        const int r = it * RPS + lane / CPW;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            pv[it][w] = lds_read_b128(lds_addr(lds + w * 2 * TILE) + r * D * 4 + ((ch ^ (r & 15)) * 16));
+            ml[it][w] = *(const float2 *)sm_ml[w][r];
+        }
+    }
+    lds_wait_any();
+#pragma unroll
+    for (int it = 0; it < NR; it++) {
+        const int r = it * RPS + lane / CPW;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, ml[it][w].x);
         const float mu = M == -INFINITY ? 0.f : M;
         float L = 0.f;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        u32x4 pv[4];
-#pragma unroll
-        for (int w = 0; w < 4; w++)
-            pv[w] = lds_read_b128(lds_addr(lds + w * 2 * TILE) + r * D * 4 + ((ch ^ (r & 15)) * 16));
-        lds_wait_any();
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            tie(pv[w]);
-            const float a = __builtin_amdgcn_exp2f(mw[w] - mu);
-            L += sm_ml[w][r][1] * a;
-            acc += __builtin_bit_cast(f32x4, pv[w]) * a;
+            tie(pv[it][w]);
+            const float a = __builtin_amdgcn_exp2f(ml[it][w].x - mu);
+            L += ml[it][w].y * a;
+            acc += __builtin_bit_cast(f32x4, pv[it][w]) * a;
         }
         const float inv = L > 0.f ? 1.0f / L : 0.f;
         if (q0 + r < S)
