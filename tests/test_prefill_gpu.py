@@ -143,6 +143,18 @@ def test_f32_cache_gqa(dev, H, Hk):
     run_f32(dev, 130, H, Hk, 64, seed=24, rows=list(range(130)))
 
 
+# Workgroup geometries of the f32 kernel: hw heads of one kv head x 4/hw row
+# blocks per unit (8:1 -> two head groups per kv head; 3:1 -> one head over
+# four row blocks, whose later rows start their windows later).
+@pytest.mark.parametrize("H,Hk,D,S,start_pos,window", [
+    (16, 2, 128, 257, 0, 0), (16, 2, 64, 190, 60, 70),
+    (6, 2, 128, 300, 0, 90), (6, 2, 64, 129, 31, 0),
+    (4, 2, 128, 250, 17, 45)])
+def test_f32_cache_workgroup_geometries(dev, H, Hk, D, S, start_pos, window):
+    run_f32(dev, S, H, Hk, D, start_pos=start_pos, window=window, seed=25,
+            rows=list(range(S)))
+
+
 def test_cfg3_pipeline_norm_rope_all_rows(dev):
     """cfg3 as BASELINE configures it, end to end at full size: raw f32 Q/K/V
     ~ N(0,1) -> fused append (per-head RMSNorm with unit weights, eps 1e-6,
