@@ -61,6 +61,14 @@ def test_window_masking(dev, S, window):
     run_case(dev, "f16", S, 8, 4, 128, window=window, seed=5)
 
 
+# cfg4's local layers with the prompt longer than the window (S > W), on the
+# head_dim-256 kernel: masking at both ends of every row's key range.
+@pytest.mark.parametrize("dtype,S,start_pos,window", [
+    ("f16", 1536, 0, 1024), ("f16", 1536, 0, 512), ("bf16", 700, 300, 333)])
+def test_head_dim_256_binding_window(dev, dtype, S, start_pos, window):
+    run_case(dev, dtype, S, 8, 4, 256, start_pos=start_pos, window=window, seed=11)
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("D", [64, 128, 256])
 def test_dtypes_head_dims(dev, dtype, D):
