@@ -244,8 +244,7 @@ __global__ __launch_bounds__(MW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel(
         }
         float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                          fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        mt = rows_max(mt);
         const float m_new = fmaxf(m_run, mt);
         const float mu = m_new == -INFINITY ? 0.f : m_new;
         if (__any(m_new != m_run)) {  // rescale only when some head's max moved
@@ -331,8 +330,7 @@ __global__ __launch_bounds__(MW * 64, D <= 128 ? 2 : 1) void decode_mfma_kernel(
     }
 
     // ---- wave result: head n16, d = dt*16 + kg*4 + i ----
-    l_part += __shfl_xor(l_part, 16, 64);
-    l_part += __shfl_xor(l_part, 32, 64);
+    l_part = rows_sum(l_part);
     if constexpr (MW == 1) {
         // One wave: its registers are the split's result, written without an
         // LDS round trip (as decode_dma_kernel's one-wave path).
@@ -576,8 +574,7 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
         }
         float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                          fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        mt = rows_max(mt);
         const float m_new = fmaxf(m_run, mt);
         const float mu = m_new == -INFINITY ? 0.f : m_new;
         if (__any(m_new != m_run)) {
@@ -655,17 +652,25 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
     }
     __builtin_amdgcn_s_waitcnt(vm_wait(0));  // drain DMA before the LDS is reused
 
-    l_part += __shfl_xor(l_part, 16, 64);
-    l_part += __shfl_xor(l_part, 32, 64);
+    l_part = rows_sum(l_part);
     if constexpr (MW == 1) {
         // One wave: its registers are the split's result (lane: head n16,
         // columns dt*16 + kg*4 .. +3), written without an LDS round trip.
         if (head_ok) {
             const int64_t u = (int64_t)b * n_units + unit;
+            if (splits == 1) {
 #pragma unroll
-            for (int dt = 0; dt < NDT; dt++)
-                store_split<D>(oacc[dt], m_run, l_part, dt * 4 + kg, n16, b, split, splits, gt,
-                               n_head, head0, u, gt * D, out, ws_ml, ws_acc);
+                for (int dt = 0; dt < NDT; dt++)
+                    store_split<D>(oacc[dt], m_run, l_part, dt * 4 + kg, n16, b, split, splits, gt,
+                                   n_head, head0, u, gt * D, out, ws_ml, ws_acc);
+            } else {
+                // The split's partial: O unnormalised, then (m, l) once per head.
+                float *ap = ws_acc + (u * splits + split) * (gt * D) + n16 * D + kg * 4;
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) *(f32x4 *)(ap + dt * 16) = oacc[dt];
+                if (kg == 0)
+                    *(float2 *)(ws_ml + ((u * splits + split) * gt + n16) * 2) = float2{m_run, l_part};
+            }
         }
         return;
     }
@@ -730,8 +735,7 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NML; j++) mx = fmaxf(mx, ml[j].x);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = wave_max(mx);
     const float mu = mx == -INFINITY ? 0.f : mx;
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -742,17 +746,14 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     // Sum the split residues: across the lanes of a wave holding one column
     // group (lane bits above the column), then across the waves.
 #pragma unroll
-    for (int o = NC; o < 64; o <<= 1)
-#pragma unroll
-        for (int i = 0; i < 4; i++) a[i] += __shfl_xor(a[i], o, 64);
+    for (int i = 0; i < 4; i++) a[i] = class_sum<NC>(a[i]);
     if (lane < NC) red[tid >> 6][col] = a;
     __syncthreads();
     if (tid < 64) {  // wave 0: the denominator, then the NC output columns
         float den = 0.f;
 #pragma unroll
         for (int j = 0; j < NML; j++) den += ml[j].y * __builtin_amdgcn_exp2f(ml[j].x - mu);
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o, 64);
+        den = wave_sum(den);
         const float inv = den > 0.f ? 1.0f / den : 0.f;
         for (int c = lane; c < NC; c += 64) {
             f32x4 t = red[0][c];

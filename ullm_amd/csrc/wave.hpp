@@ -39,6 +39,42 @@ __device__ __forceinline__ float wave_sum(float x) {
     return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 
+// max / sum of x over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows),
+// in VALU only (the gfx950 row swaps), every lane getting the result.
+__device__ __forceinline__ float rows_max(float x) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// Full-wave max in VALU only (as wave_sum).
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp<kDppXor1>(x));
+    x = fmaxf(x, dpp<kDppXor2>(x));
+    x = fmaxf(x, dpp<kDppHalfMirror>(x));
+    x = fmaxf(x, dpp<kDppMirror>(x));
+    return rows_max(x);
+}
+
+// Sum over the lanes congruent to l modulo N (N a power of two, 1 <= N <= 16):
+// row rotations by N, 2N, .. 8 inside each 16-lane row, then the row swaps.
+template <int N>
+__device__ __forceinline__ float class_sum(float x) {
+    static_assert(N >= 1 && N <= 16 && (N & (N - 1)) == 0, "class size");
+    if constexpr (N <= 1) x += dpp<0x121>(x);
+    if constexpr (N <= 2) x += dpp<0x122>(x);
+    if constexpr (N <= 4) x += dpp<0x124>(x);
+    if constexpr (N <= 8) x += dpp<0x128>(x);  // row_ror:8 = lane ^ 8 in the row
+    return rows_sum(x);
+}
+
 // The value of lane l ^ 32.
 __device__ __forceinline__ float xor32(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
