@@ -23,6 +23,7 @@
 //  * Softmax runs in the exp2 domain: q is pre-multiplied by scale*log2(e).
 #include "common.hpp"
 #include "wave.hpp"
+#include "mfma_util.hpp"
 #include <cstdlib>
 #include <algorithm>
 #include <mutex>
@@ -165,25 +166,51 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 1) void decode_split_kernel(
         }
     }
 
-    // Merge the lane groups of this wave (lanes sub, sub+LPT, ...).
-#pragma unroll
-    for (int off = LPT; off < 64; off <<= 1) {
+    // Merge the lane groups of this wave (lanes sub, sub+LPT, ...): a
+    // butterfly over lane ^ LPT, .. lane ^ 32.  At 16 and 32 the row swaps
+    // hand every lane both states of its pair in registers (the merge is
+    // symmetric, so their order does not matter); below 16, shuffles.
+    auto merge_pair = [&](int g, float m0, float l0, float m1, float l1, float &a, float &c) {
+        const float mn = fmaxf(m0, m1);
+        const float mu = (mn == -INFINITY) ? 0.f : mn;
+        a = exp2f(m0 - mu);
+        c = exp2f(m1 - mu);
+        l[g] = l0 * a + l1 * c;
+        m[g] = mn;
+    };
+    auto swap16 = [](float x) {
+        return __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    };
+    auto swap32 = [](float x) {
+        return __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    };
+    auto merge_rows = [&](auto swp) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            const float mo = __shfl_xor(m[g], off, 64);
-            const float lo = __shfl_xor(l[g], off, 64);
-            const float mn = fmaxf(m[g], mo);
-            const float mu = (mn == -INFINITY) ? 0.f : mn;
-            const float a = exp2f(m[g] - mu), c = exp2f(mo - mu);
-            l[g] = l[g] * a + lo * c;
-            m[g] = mn;
+            const auto mm = swp(m[g]), ll = swp(l[g]);
+            float a, c;
+            merge_pair(g, __uint_as_float(mm[0]), __uint_as_float(ll[0]), __uint_as_float(mm[1]),
+                       __uint_as_float(ll[1]), a, c);
 #pragma unroll
             for (int e = 0; e < EPL; e++) {
-                const float ao = __shfl_xor(acc[g][e], off, 64);
-                acc[g][e] = acc[g][e] * a + ao * c;
+                const auto aa = swp(acc[g][e]);
+                acc[g][e] = __uint_as_float(aa[0]) * a + __uint_as_float(aa[1]) * c;
             }
         }
+    };
+#pragma unroll
+    for (int off = LPT; off < 16; off <<= 1) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float mo = __shfl_xor(m[g], off, 64), lo = __shfl_xor(l[g], off, 64);
+            float a, c;
+            merge_pair(g, m[g], l[g], mo, lo, a, c);
+#pragma unroll
+            for (int e = 0; e < EPL; e++) acc[g][e] = acc[g][e] * a + __shfl_xor(acc[g][e], off, 64) * c;
+        }
     }
+    if constexpr (LPT <= 16) merge_rows(swap16);
+    if constexpr (LPT <= 32) merge_rows(swap32);
 
     // Merge the waves through LDS.
     constexpr int kAccFloats = NW * G * D;

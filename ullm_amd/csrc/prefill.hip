@@ -291,7 +291,7 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
 #pragma unroll
             for (int i = 0; i < 16; i++) m4[i & 3] = fmaxf(m4[i & 3], sacc[kt][i]);
         float mloc = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * qscale;
+        mloc = fmaxf(mloc, xor32(mloc)) * qscale;
         const float m_new = fmaxf(m_run, mloc);
         const float mu = m_new == -INFINITY ? 0.f : m_new;
         if (__any(m_new != m_run)) {
@@ -346,7 +346,7 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
     __builtin_amdgcn_s_waitcnt(vm_wait(0));  // no DMA may outlive the workgroup
 
     if (!active) return;
-    const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+    const float l_tot = l_part + xor32(l_part);
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     const int qrow = row0 + c32;
     if (qrow >= S) return;
@@ -742,7 +742,7 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
             pv(par);
             const float m_next = rowmax(npar);
             if (set == 0 && gB >= 0 && j == TA - 1) {  // block A complete: write it, switch to B
-                const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+                const float l_tot = l_part + xor32(l_part);
                 const float inv = 1.0f / l_tot;
                 const int qrow = rowA + sub + c32;
                 if (qrow < S) {
@@ -781,7 +781,7 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     wg_barrier();  // ring idle
     const uint32_t part = lds0 + (slot * 64 + lane) * 16;  // [slot][dt][g][lane] f32x4
     if (set == 1) {
-        const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+        const float l_tot = l_part + xor32(l_part);
         if (h2 == 0) { hand_ml[slot][c32][0] = m_run; hand_ml[slot][c32][1] = l_tot; }
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++)
@@ -795,7 +795,7 @@ __global__ __launch_bounds__(512) void prefill4_kernel(
     wg_barrier();
     const uint32_t stg = lds0 + 4 * 64 * NDT * 64;  // staged rows [32][OROW]
     if (set == 0) {
-        const float l0 = l_part + __shfl_xor(l_part, 32, 64);
+        const float l0 = l_part + xor32(l_part);
         const float m1 = hand_ml[slot][c32][0], l1 = hand_ml[slot][c32][1];
         const float M = fmaxf(m_run, m1);
         const float mu = M == -INFINITY ? 0.f : M;
@@ -1011,7 +1011,7 @@ __global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
             sacc[i] = sv;
             mloc = fmaxf(mloc, sv);
         }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        mloc = fmaxf(mloc, xor32(mloc));
         // Lazy max: raised only when a row's tile max passes it by 2^kLazy
         // (P = exp2(s - m) <= 256 stays exact in f16's range), so the O
         // rescale (128 accumulators) runs a few times per wave, not per tile.
@@ -1093,7 +1093,7 @@ __global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
     __builtin_amdgcn_s_waitcnt(vm_wait(0));
 
     // ---- merge the 4 partials through LDS (each wave's own stages) ----
-    const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+    const float l_tot = l_part + xor32(l_part);
     if (h2 == 0) { sm_ml[wave][c][0] = m_run; sm_ml[wave][c][1] = l_tot; }
     // lane (c, h2) holds row c, d = dt*32 + g*8 + h2*4 + 0..3: chunk dt*8 + g*2 + h2,
     // stored at chunk ^ (row % 16) of a D-float row.
@@ -1381,7 +1381,7 @@ __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(
     };
     // O^T in registers: lane (row c, h2) holds d = dt*32 + 8g + 4*h2 + 0..3.
     auto end_unit = [&]() {
-        const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+        const float l_tot = l_part + xor32(l_part);
         const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
         if (qrow < S) {
             float *op = out + (int64_t)qrow * q_dim + (int64_t)head * D + h2 * 4;

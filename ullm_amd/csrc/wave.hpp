@@ -1,6 +1,7 @@
 // Wavefront-level reductions for wave64 (gfx950).  Reductions inside a
 // 16-lane row use DPP modifiers (one VALU op per step); wider steps use
-// ds_bpermute through __shfl_xor.
+// the gfx950 row swaps (v_permlane16_swap / v_permlane32_swap): no LDS round
+// trips.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -21,8 +22,14 @@ __device__ __forceinline__ float group_sum(float x) {
     if constexpr (N >= 4) x += dpp<kDppXor2>(x);
     if constexpr (N >= 8) x += dpp<kDppHalfMirror>(x);
     if constexpr (N >= 16) x += dpp<kDppMirror>(x);
-    if constexpr (N >= 32) x += __shfl_xor(x, 16, 64);
-    if constexpr (N >= 64) x += __shfl_xor(x, 32, 64);
+    if constexpr (N >= 32) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    if constexpr (N >= 64) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
     return x;
 }
 
@@ -79,6 +86,21 @@ __device__ __forceinline__ float class_sum(float x) {
 __device__ __forceinline__ float xor32(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+}
+
+// The value of lane l ^ OFF, OFF in {8, 16, 32}, without an LDS round trip
+// (8: a row rotation by 8 within each 16-lane row, which is l ^ 8 there).
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float x) {
+    static_assert(OFF == 8 || OFF == 16 || OFF == 32, "lane_xor offset");
+    if constexpr (OFF == 8) {
+        return dpp<0x128>(x);
+    } else if constexpr (OFF == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+    } else {
+        return xor32(x);
+    }
 }
 
 }  // namespace ullm
