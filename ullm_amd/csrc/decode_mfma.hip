@@ -699,13 +699,15 @@ constexpr int kMaxSplits = 256;
 // wave forms the maximum and the denominator by itself.  The only LDS round
 // trip is the final sum of the R split residues across the waves.
 // NL = partial rows per thread, ceil(splits / R).
-constexpr int kMergeThreads = 256;
+// MT = threads: 64 (one wave, no LDS step, when NL <= 16 rows per lane
+// cover the splits) or 256.
 constexpr int kMergeGroups = 4;
 // NML = (m, l) pairs per lane, ceil(splits / 64).
-template <int D, int NL, int NML>
-__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
+template <int D, int NL, int NML, int MT>
+__global__ __launch_bounds__(MT) void decode_merge_kernel(
     const float *__restrict__ ws_ml, const float *__restrict__ ws_acc, int splits, int gt,
     int n_units, int n_head, float *__restrict__ out) {
+    constexpr int kMergeThreads = MT;
     constexpr int NC = D / 4 / kMergeGroups, R = kMergeThreads / NC;
     static_assert(NML * 64 <= kMaxSplits, "merge reads at most kMaxSplits (m, l) pairs");
     const int g = blockIdx.x / kMergeGroups, cg = blockIdx.x % kMergeGroups;
@@ -747,6 +749,17 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     // group (lane bits above the column), then across the waves.
 #pragma unroll
     for (int i = 0; i < 4; i++) a[i] = class_sum<NC>(a[i]);
+    if constexpr (kMergeThreads == 64) {
+        // One wave: every lane holds its column group's total.
+        float den = 0.f;
+#pragma unroll
+        for (int j = 0; j < NML; j++) den += ml[j].y * __builtin_amdgcn_exp2f(ml[j].x - mu);
+        den = wave_sum(den);
+        const float inv = den > 0.f ? 1.0f / den : 0.f;
+        if (lane < NC)
+            *(f32x4 *)(out + ((int64_t)b * n_head + unit * gt + g) * D + c4 * 4) = a * inv;
+        return;
+    }
     if (lane < NC) red[tid >> 6][col] = a;
     __syncthreads();
     if (tid < 64) {  // wave 0: the denominator, then the NC output columns
@@ -867,29 +880,34 @@ struct MainLaunch<T, D, false> {
 
 template <int D>
 static void launch_merge(const MfmaPlan &p, int batch, int nh, float *out, char *ws, hipStream_t st) {
-    constexpr int R = kMergeThreads / (D / 4 / kMergeGroups);
-    const int nl = (p.splits + R - 1) / R;
+    constexpr int NC = D / 4 / kMergeGroups;
     const dim3 g(p.gt * kMergeGroups, p.n_units, batch);
     const float *ml = (const float *)(ws + p.off_ml), *ac = (const float *)(ws + p.off_acc);
     // (m, l) loads per lane: as many as the splits need, not kMaxSplits / 64.
-    auto go = [&](auto nlc) {
-        constexpr int NL = decltype(nlc)::value;
+    auto go = [&](auto nlc, auto mtc) {
+        constexpr int NL = decltype(nlc)::value, MT = decltype(mtc)::value;
         if (p.splits <= 64)
-            hipLaunchKernelGGL((decode_merge_kernel<D, NL, 1>), g, dim3(kMergeThreads), 0, st, ml,
-                               ac, p.splits, p.gt, p.n_units, nh, out);
+            hipLaunchKernelGGL((decode_merge_kernel<D, NL, 1, MT>), g, dim3(MT), 0, st, ml, ac,
+                               p.splits, p.gt, p.n_units, nh, out);
         else if (p.splits <= 128)
-            hipLaunchKernelGGL((decode_merge_kernel<D, NL, 2>), g, dim3(kMergeThreads), 0, st, ml,
-                               ac, p.splits, p.gt, p.n_units, nh, out);
+            hipLaunchKernelGGL((decode_merge_kernel<D, NL, 2, MT>), g, dim3(MT), 0, st, ml, ac,
+                               p.splits, p.gt, p.n_units, nh, out);
         else
-            hipLaunchKernelGGL((decode_merge_kernel<D, NL, kMaxSplits / 64>), g,
-                               dim3(kMergeThreads), 0, st, ml, ac, p.splits, p.gt, p.n_units, nh,
-                               out);
+            hipLaunchKernelGGL((decode_merge_kernel<D, NL, kMaxSplits / 64, MT>), g, dim3(MT), 0,
+                               st, ml, ac, p.splits, p.gt, p.n_units, nh, out);
     };
-    if (nl <= 1) go(Int<1>{});
-    else if (nl <= 2) go(Int<2>{});
-    else if (nl <= 4) go(Int<4>{});
-    else if (nl <= 8) go(Int<8>{});
-    else go(Int<16>{});
+    // One wave (no LDS step) when 4 split rows per lane cover the splits;
+    // with more, four waves keep the rows per lane, hence the serial loads,
+    // low (one wave with 16 rows measured 0.25 us slower at cfg2's 128
+    // splits; at cfg1's 16 it is 0.15 us faster).
+    constexpr int R1 = 64 / NC, R4 = 256 / NC;
+    const int nl1 = (p.splits + R1 - 1) / R1, nl4 = (p.splits + R4 - 1) / R4;
+    if (nl1 <= 4) go(Int<4>{}, Int<64>{});
+    else if (nl4 <= 1) go(Int<1>{}, Int<256>{});
+    else if (nl4 <= 2) go(Int<2>{}, Int<256>{});
+    else if (nl4 <= 4) go(Int<4>{}, Int<256>{});
+    else if (nl4 <= 8) go(Int<8>{}, Int<256>{});
+    else go(Int<16>{}, Int<256>{});
 }
 
 void decode_merge_launch(int D, const float *ws_ml, const float *ws_acc, int splits, int gt,
