@@ -752,7 +752,7 @@ def main():
                      "frac": round(d["gbps_step"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("bytes_per_launch") if traffic else None,
                      "traffic_measured_at": traffic.get("commit") if traffic else None,
-                     "kernel": "decode_dma_kernel<F16,128,1> + decode_merge_kernel<128,2> "
+                     "kernel": "decode_dma_kernel<F16,128,1> + decode_merge_kernel<128,4,2,256> "
                                "(one decode-attention op per layer)",
                      "algorithmic_bytes": int(d["layer_bytes"]),
                      "us_per_launch": round(d["us_per_layer"], 3),
