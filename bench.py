@@ -186,7 +186,11 @@ def bench_prefill(torch, A, args, S, H, Hk, D, dt, window=0, first=None):
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / (n * reps)
     n = n * reps
-    flop = 4.0 * D * H * S * (S + 1) / 2  # causal pairs only (window >= S here)
+    # (query, key) pairs the mask keeps: row i sees min(i + 1, window) keys
+    pairs = S * (S + 1) / 2
+    if 0 < window < S:
+        pairs -= (S - window) * (S - window + 1) / 2
+    flop = 4.0 * D * H * pairs
     res = dict(ms=ms, tflops=flop / (ms * 1e-3) / 1e12, flop=flop, launches=n)
     if first is not None:
         run()
@@ -619,6 +623,10 @@ def main():
                                    windows=[1024] * 5 + [0])
         res["cfg4_prefill"] = bench_prefill(torch, A, args, 1024, 8, 4, 256, torch.float16,
                                             window=1024)
+        # A long prompt: the global layer and a sliding-window layer at S=8192.
+        res["cfg4_prefill_8k"] = bench_prefill(torch, A, args, 8192, 8, 4, 256, torch.float16)
+        res["cfg4_prefill_8k_w"] = bench_prefill(torch, A, args, 8192, 8, 4, 256, torch.float16,
+                                                 window=1024)
     if want("append"):
         res["append"] = bench_append(torch, A, args, 2048, 32, 8, 128, torch.bfloat16)
     if want("proj"):
@@ -698,6 +706,18 @@ def main():
                          "ms": round(c4p["ms"], 4), "tflops": round(c4p["tflops"], 2),
                          "flop_causal": c4p["flop"],
                          "frac_mfma": round(c4p["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "cfg4_prefill_8k": {"workload": "cfg4 shapes at an 8192-token prompt: 8/4 heads, "
+                                        "head_dim 256, f16; global layer (causal) and a "
+                                        "sliding-window layer (window 1024)",
+                            "kernel": "prefill_shared_kernel<F16>",
+                            "global": {"ms": round(res["cfg4_prefill_8k"]["ms"], 4),
+                                       "tflops": round(res["cfg4_prefill_8k"]["tflops"], 2),
+                                       "frac_mfma": round(res["cfg4_prefill_8k"]["tflops"]
+                                                          / MFMA_BF16_PEAK_TFLOPS, 4)},
+                            "window_1024": {"ms": round(res["cfg4_prefill_8k_w"]["ms"], 4),
+                                            "tflops": round(res["cfg4_prefill_8k_w"]["tflops"], 2),
+                                            "frac_mfma": round(res["cfg4_prefill_8k_w"]["tflops"]
+                                                               / MFMA_BF16_PEAK_TFLOPS, 4)}},
         "f32_prefill": {"workload": "cfg3 shape (S=2048, 32/8 heads, head_dim 128) over an f32 "
                                     "cache, the reference's own cache dtype: Q.K on bf16 hi + lo "
                                     "halves of Q and K, P.V in f16",

@@ -69,6 +69,48 @@ def test_head_dim_256_binding_window(dev, dtype, S, start_pos, window):
     run_case(dev, dtype, S, 8, 4, 256, start_pos=start_pos, window=window, seed=11)
 
 
+def shared_tiles_path(S, start_pos, window, H, Hk):
+    """Whether head_dim-256 prefill takes prefill_shared_kernel: the rule of
+    prefill_shared_applies (prefill_shared.hip), restated to show which
+    kernel a test case runs."""
+    kv_mul, hw = H // Hk, 1
+    while hw < 4 and kv_mul % (hw * 2) == 0:
+        hw *= 2
+    UR = 128 // hw
+    nts = []
+    for u in range((S + UR - 1) // UR):
+        r0 = u * UR
+        hi = start_pos + min(r0 + UR, S)
+        lo = max(0, start_pos + r0 + 1 - window) if window > 0 else 0
+        nts.append((hi + 31) // 32 - lo // 32)
+    return max(nts) * 256 * 2 <= 7 * sum(nts) * (H // hw)
+
+
+# head_dim 256 on the shared-tile kernel (long prompts, many heads): every
+# workgroup geometry (hw = 4, 2, 1 with kv_mul 8/4, 2, 3 and 1), windows,
+# start_pos and lengths that end inside a unit.
+@pytest.mark.parametrize("dtype,S,H,Hk,start_pos,window", [
+    ("f16", 4096, 8, 4, 0, 1024),    # cfg4's local layers at S=4096
+    ("bf16", 4096, 8, 4, 0, 0),      # and its global layer
+    ("f16", 1000, 16, 4, 37, 200),
+    ("bf16", 777, 32, 4, 0, 0),
+    ("bf16", 1024, 16, 16, 100, 128),
+    ("f16", 2048, 12, 4, 0, 256),
+    ("bf16", 3000, 16, 8, 500, 0),
+    ("f16", 600, 32, 16, 0, 100)])
+def test_head_dim_256_shared_tiles(dev, dtype, S, H, Hk, start_pos, window):
+    assert shared_tiles_path(S, start_pos, window, H, Hk)
+    run_case(dev, dtype, S, H, Hk, 256, start_pos=start_pos, window=window, seed=12)
+
+
+def test_head_dim_256_path_split():
+    """The cfg4 prefill as configured stays on prefill_sk_kernel; the shapes
+    above and one binding-window case take the shared-tile kernel."""
+    assert not shared_tiles_path(1024, 0, 1024, 8, 4)
+    assert not shared_tiles_path(1536, 0, 1024, 8, 4)
+    assert shared_tiles_path(1536, 0, 512, 8, 4)
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("D", [64, 128, 256])
 def test_dtypes_head_dims(dev, dtype, D):

@@ -1615,6 +1615,9 @@ extern "C" int ullm_hip_attn_prefill(const void *q, const void *k_cache, const v
             return launch_prefill_f32<64>(q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
         return launch_prefill_f32<128>(q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
     }
+    if (head_dim == 256 && prefill_shared_applies(S, start_pos, window, n_head, kv_mul))
+        return launch_prefill_shared(dtype, q, k_cache, v_cache, kv_stride, S, start_pos, window,
+                                     n_head, kv_mul, qs, out, st);
     if (dtype == ULLM_DT_BF16)
         return dispatch_prefill<BF16>(head_dim, q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
     return dispatch_prefill<F16>(head_dim, q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
