@@ -69,27 +69,28 @@ def test_head_dim_256_binding_window(dev, dtype, S, start_pos, window):
     run_case(dev, dtype, S, 8, 4, 256, start_pos=start_pos, window=window, seed=11)
 
 
-def shared_tiles_path(S, start_pos, window, H, Hk):
-    """Whether head_dim-256 prefill takes prefill_shared_kernel: the rule of
-    prefill_shared_applies (prefill_shared.hip), restated to show which
-    kernel a test case runs."""
-    kv_mul, hw = H // Hk, 1
-    while hw < 4 and kv_mul % (hw * 2) == 0:
-        hw *= 2
-    UR = 128 // hw
-    nts = []
-    for u in range((S + UR - 1) // UR):
-        r0 = u * UR
-        hi = start_pos + min(r0 + UR, S)
-        lo = max(0, start_pos + r0 + 1 - window) if window > 0 else 0
-        nts.append((hi + 31) // 32 - lo // 32)
-    return max(nts) * 256 * 2 <= 7 * sum(nts) * (H // hw)
+def p16_geometry(S, H, Hk):
+    """(key streams, heads per workgroup) of prefill16_kernel for a
+    head_dim-256 prompt: the rule of prefill16_streams / p16_hw
+    (prefill16.hip), restated to show which workgroup geometry a test case
+    runs."""
+    kv_mul = H // Hk
+
+    def hw_of(nws):
+        hw = 1
+        while hw < nws and hw < 4 and kv_mul % (hw * 2) == 0:
+            hw *= 2
+        return hw
+    hw1 = hw_of(8)
+    units = (S + 128 // hw1 - 1) // (128 // hw1)
+    ks = 2 if units * (H // hw1) < 256 else 1
+    return ks, hw_of(8 // ks)
 
 
-# head_dim 256 on the shared-tile kernel (long prompts, many heads): every
-# workgroup geometry (hw = 4, 2, 1 with kv_mul 8/4, 2, 3 and 1), windows,
-# start_pos and lengths that end inside a unit.
-@pytest.mark.parametrize("dtype,S,H,Hk,start_pos,window", [
+# head_dim 256 (prefill16_kernel): every workgroup geometry -- one or two key
+# streams times 4, 2 or 1 heads per workgroup (kv_mul 8/4, 2, 3 and 1) --
+# with windows, start_pos and lengths that end inside a unit.
+P16_CASES = [
     ("f16", 4096, 8, 4, 0, 1024),    # cfg4's local layers at S=4096
     ("bf16", 4096, 8, 4, 0, 0),      # and its global layer
     ("f16", 1000, 16, 4, 37, 200),
@@ -97,18 +98,26 @@ def shared_tiles_path(S, start_pos, window, H, Hk):
     ("bf16", 1024, 16, 16, 100, 128),
     ("f16", 2048, 12, 4, 0, 256),
     ("bf16", 3000, 16, 8, 500, 0),
-    ("f16", 600, 32, 16, 0, 100)])
-def test_head_dim_256_shared_tiles(dev, dtype, S, H, Hk, start_pos, window):
-    assert shared_tiles_path(S, start_pos, window, H, Hk)
+    ("f16", 600, 32, 16, 0, 100),
+    ("f16", 1024, 8, 4, 0, 1024),    # cfg4 as configured
+    ("bf16", 333, 8, 1, 17, 0),
+    ("f16", 257, 6, 2, 3, 40),
+    ("bf16", 2500, 32, 8, 0, 0),
+    ("f16", 1, 8, 4, 0, 0),
+    ("bf16", 17, 16, 16, 5, 0),
+    ("f16", 2100, 16, 16, 0, 0)]
+
+
+@pytest.mark.parametrize("dtype,S,H,Hk,start_pos,window", P16_CASES)
+def test_head_dim_256_geometries(dev, dtype, S, H, Hk, start_pos, window):
     run_case(dev, dtype, S, H, Hk, 256, start_pos=start_pos, window=window, seed=12)
 
 
-def test_head_dim_256_path_split():
-    """The cfg4 prefill as configured stays on prefill_sk_kernel; the shapes
-    above and one binding-window case take the shared-tile kernel."""
-    assert not shared_tiles_path(1024, 0, 1024, 8, 4)
-    assert not shared_tiles_path(1536, 0, 1024, 8, 4)
-    assert shared_tiles_path(1536, 0, 512, 8, 4)
+def test_head_dim_256_geometries_covered():
+    """The cases above reach both key-stream counts with 4, 2 and 1 heads per
+    workgroup."""
+    seen = {p16_geometry(S, H, Hk) for (_, S, H, Hk, _, _) in P16_CASES}
+    assert {(1, 4), (1, 2), (1, 1), (2, 4), (2, 2), (2, 1)} <= seen, seen
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])

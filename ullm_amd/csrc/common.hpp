@@ -116,11 +116,6 @@ int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64
                 int64_t ss, const int32_t *lens, int max_len, int win, int batch, int nh, int nkv,
                 int D, float qs, float *out, void *ws, size_t ws_bytes, hipStream_t st);
 
-// Head_dim-256 prefill with K/V tiles shared by a workgroup (prefill_shared.hip).
-bool prefill_shared_applies(int S, int start_pos, int window, int n_head, int kv_mul);
-int launch_prefill_shared(int dtype, const void *q, const void *kc, const void *vc, int64_t kvs,
-                          int S, int start_pos, int window, int n_head, int kv_mul, float qs,
-                          float *out, hipStream_t st);
 // f32-cache split-KV decode over a paged cache (decode.hip).
 size_t decode_f32_workspace(int batch, int n_head, int n_kv_head, int D, int max_len, int window);
 int decode_f32_paged(const float *q, const void *kp, const void *vp, int64_t kvs,

@@ -191,4 +191,38 @@ __device__ __forceinline__ void wg_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Paged K/V (tab == nullptr: the contiguous cache).  Key t of the sequence
+// is row t % P of page tab[t / P] (P = 2^shift, a multiple of every prefill
+// kernel's key tile), so a tile's DMA goes through a buffer resource based at its page
+// whose range ends at the sequence length: rows past it, and pages outside
+// the table or [0, n_pages), read as zeros.
+struct KvPages {
+    const int32_t *tab;
+    int tab_len, shift, n_pages;
+};
+
+// Buffer resources and scalar offset of the key tile starting at key0 (a
+// tile never crosses a page).
+template <int D>
+__device__ __forceinline__ void page_tile(const KvPages &pg, const char *kc, const char *vc,
+                                          int kvh, int rbg, int kv_len, int key0,
+                                          __amdgpu_buffer_rsrc_t &kr, __amdgpu_buffer_rsrc_t &vr,
+                                          int &so) {
+    const int pi = key0 >> pg.shift;
+    const int phys = key0 < kv_len && pi < pg.tab_len ? pg.tab[pi] : -1;
+    const bool ok = phys >= 0 && phys < pg.n_pages;
+    const int64_t pb = ((int64_t)(ok ? phys : 0) << pg.shift) * rbg + (int64_t)kvh * D * 2;
+    const int rows = min(1 << pg.shift, kv_len - (pi << pg.shift));
+    const int range = ok ? (rows - 1) * rbg + D * 2 : 0;
+    kr = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + pb), 0, range, kRsrcWord3);
+    vr = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + pb), 0, range, kRsrcWord3);
+    so = __builtin_amdgcn_readfirstlane((key0 & ((1 << pg.shift) - 1)) * rbg);
+}
+
+// Head_dim-256 prefill on 16-row waves, two per SIMD (prefill16.hip);
+// pgs.tab == nullptr for a contiguous cache.
+int launch_prefill16(int dtype, const void *q, const void *kc, const void *vc, int64_t kvs, int S,
+                     int start_pos, int window, int n_head, int kv_mul, float qs, float *out,
+                     hipStream_t st, KvPages pgs);
+
 }  // namespace ullm

@@ -17,7 +17,9 @@
 //  * prefill2_kernel (head_dim <= 128, binding sliding window): the same
 //    staging without the split;
 //  * prefill_sk_kernel (head_dim 256): one 32-row block of one head per
-//    workgroup, split-K over its 4 waves, merged through LDS.
+//    workgroup, split-K over its 4 waves, merged through LDS.  Kept as a
+//    comparison point (ULLM_HIP_PREFILL256=1): head_dim 256 runs
+//    prefill16_kernel (prefill16.hip), faster at every measured shape.
 // In every kernel the S^T = K.Q^T accumulator holds ONE query row per lane
 // (lane % 32) and 16 keys, so the row max needs a single cross-lane exchange
 // (lane ^ 32); exponentiated and rounded to f16 it IS the B operand of
@@ -82,33 +84,6 @@ struct PF2 {
     static constexpr int NDT = D / 32;              // output d tiles
     static_assert(NIW >= 1 && NI % NW == 0, "DMA split");
 };
-
-// Paged K/V (tab == nullptr: the contiguous cache).  Key t of the sequence
-// is row t % P of page tab[t / P] (P = 2^shift, a multiple of the 64-key
-// tile), so a tile's DMA goes through a buffer resource based at its page
-// whose range ends at the sequence length: rows past it, and pages outside
-// the table or [0, n_pages), read as zeros.
-struct KvPages {
-    const int32_t *tab;
-    int tab_len, shift, n_pages;
-};
-
-// Buffer resources and scalar offset of the 64-key tile starting at key0.
-template <int D>
-__device__ __forceinline__ void page_tile(const KvPages &pg, const char *kc, const char *vc,
-                                          int kvh, int rbg, int kv_len, int key0,
-                                          __amdgpu_buffer_rsrc_t &kr, __amdgpu_buffer_rsrc_t &vr,
-                                          int &so) {
-    const int pi = key0 >> pg.shift;
-    const int phys = key0 < kv_len && pi < pg.tab_len ? pg.tab[pi] : -1;
-    const bool ok = phys >= 0 && phys < pg.n_pages;
-    const int64_t pb = ((int64_t)(ok ? phys : 0) << pg.shift) * rbg + (int64_t)kvh * D * 2;
-    const int rows = min(1 << pg.shift, kv_len - (pi << pg.shift));
-    const int range = ok ? (rows - 1) * rbg + D * 2 : 0;
-    kr = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + pb), 0, range, kRsrcWord3);
-    vr = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + pb), 0, range, kRsrcWord3);
-    so = __builtin_amdgcn_readfirstlane((key0 & ((1 << pg.shift) - 1)) * rbg);
-}
 
 template <class T, int D>
 __global__ __launch_bounds__(512) void prefill2_kernel(
@@ -1146,13 +1121,21 @@ __global__ __launch_bounds__(256, 1) void prefill_sk_kernel(
     }
 }
 
-// head_dim 256: split-K inside one-wave-per-SIMD workgroups (the shared-ring
-// kernels need more than the 256 registers two waves per SIMD allow).
+// head_dim 256: prefill16_kernel (16-row waves, two per SIMD), or on request
+// prefill_sk_kernel (split-K inside one-wave-per-SIMD workgroups).
 template <class T, int D, bool V2 = (D <= 128)>
 struct PrefillLaunch {
     static void run(const void *q, const void *kc, const void *vc, int64_t kvs, int S, int sp,
                     int win, int nh, int kv_mul, float qs, float *out, hipStream_t st,
                     KvPages pgs = KvPages{}) {
+        // prefill16_kernel; ULLM_HIP_PREFILL256=1 selects prefill_sk_kernel
+        // instead, for comparison.
+        static const int pick = env_override("ULLM_HIP_PREFILL256");
+        if (pick != 1) {
+            launch_prefill16(__is_same(T, BF16) ? ULLM_DT_BF16 : ULLM_DT_F16, q, kc, vc, kvs, S, sp,
+                             win, nh, kv_mul, qs, out, st, pgs);
+            return;
+        }
         const int nb = (S + 31) / 32;
         const int total = nh * nb;
         const int per_xcd = (total + 7) / 8;
@@ -1615,9 +1598,6 @@ extern "C" int ullm_hip_attn_prefill(const void *q, const void *k_cache, const v
             return launch_prefill_f32<64>(q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
         return launch_prefill_f32<128>(q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
     }
-    if (head_dim == 256 && prefill_shared_applies(S, start_pos, window, n_head, kv_mul))
-        return launch_prefill_shared(dtype, q, k_cache, v_cache, kv_stride, S, start_pos, window,
-                                     n_head, kv_mul, qs, out, st);
     if (dtype == ULLM_DT_BF16)
         return dispatch_prefill<BF16>(head_dim, q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
     return dispatch_prefill<F16>(head_dim, q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
