@@ -702,14 +702,14 @@ def main():
                         "frac_hbm": round(c4["gbps_step"] / HBM_PEAK_GBS, 4)},
         "cfg4_prefill": {"workload": "cfg4 causal prefill, S=1024, 8/4 heads, head_dim 256, "
                                      "f16, window 1024 (= causal at this length)",
-                         "kernel": "prefill16_kernel<F16,2> (two key streams)",
+                         "kernel": "prefill16_kernel<F16,2,2> (two key streams, value columns split over two workgroups)",
                          "ms": round(c4p["ms"], 4), "tflops": round(c4p["tflops"], 2),
                          "flop_causal": c4p["flop"],
                          "frac_mfma": round(c4p["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)},
         "cfg4_prefill_8k": {"workload": "cfg4 shapes at an 8192-token prompt: 8/4 heads, "
                                         "head_dim 256, f16; global layer (causal) and a "
                                         "sliding-window layer (window 1024)",
-                            "kernel": "prefill16_kernel<F16,1> (one key stream)",
+                            "kernel": "prefill16_kernel<F16,1,1> (one key stream)",
                             "global": {"ms": round(res["cfg4_prefill_8k"]["ms"], 4),
                                        "tflops": round(res["cfg4_prefill_8k"]["tflops"], 2),
                                        "frac_mfma": round(res["cfg4_prefill_8k"]["tflops"]

@@ -69,9 +69,9 @@ def test_head_dim_256_binding_window(dev, dtype, S, start_pos, window):
     run_case(dev, dtype, S, 8, 4, 256, start_pos=start_pos, window=window, seed=11)
 
 
-def p16_geometry(S, H, Hk):
-    """(key streams, heads per workgroup) of prefill16_kernel for a
-    head_dim-256 prompt: the rule of prefill16_streams / p16_hw
+def p16_geometry(S, H, Hk, start_pos=0, window=0):
+    """(key streams, heads per workgroup, value split) of prefill16_kernel
+    for a head_dim-256 prompt: the rule of prefill16_plan / p16_hw
     (prefill16.hip), restated to show which workgroup geometry a test case
     runs."""
     kv_mul = H // Hk
@@ -82,9 +82,13 @@ def p16_geometry(S, H, Hk):
             hw *= 2
         return hw
     hw1 = hw_of(8)
-    units = (S + 128 // hw1 - 1) // (128 // hw1)
-    ks = 2 if units * (H // hw1) < 256 else 1
-    return ks, hw_of(8 // ks)
+    grid1 = (S + 128 // hw1 - 1) // (128 // hw1) * (H // hw1)
+    binding = 0 < window < start_pos + S
+    ks = 2 if grid1 < 256 or (grid1 == 256 and not binding) else 1
+    hw = hw_of(8 // ks)
+    ur = 16 * (8 // ks) // hw
+    ds = 2 if ks == 2 and (S + ur - 1) // ur * (H // hw) * 2 <= 256 else 1
+    return ks, hw, ds
 
 
 # head_dim 256 (prefill16_kernel): every workgroup geometry -- one or two key
@@ -115,9 +119,10 @@ def test_head_dim_256_geometries(dev, dtype, S, H, Hk, start_pos, window):
 
 def test_head_dim_256_geometries_covered():
     """The cases above reach both key-stream counts with 4, 2 and 1 heads per
-    workgroup."""
-    seen = {p16_geometry(S, H, Hk) for (_, S, H, Hk, _, _) in P16_CASES}
-    assert {(1, 4), (1, 2), (1, 1), (2, 4), (2, 2), (2, 1)} <= seen, seen
+    workgroup, and the value split with two key streams at each head count."""
+    seen = {p16_geometry(S, H, Hk, sp, w) for (_, S, H, Hk, sp, w) in P16_CASES}
+    assert {(1, 4, 1), (1, 2, 1), (1, 1, 1), (2, 4, 1), (2, 2, 1), (2, 1, 1),
+            (2, 4, 2), (2, 2, 2), (2, 1, 2)} <= seen, seen
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])

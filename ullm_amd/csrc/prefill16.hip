@@ -31,6 +31,10 @@
 // unit's key range is cut in two halves, one per stream, and the two partial
 // (m, l, O) of every row are merged through LDS at the end: twice the
 // workgroups for a short prompt, where whole units would leave CUs idle.
+// With DS = 2 two workgroups share a unit: each computes the full Q.K and
+// softmax but P.V and the output for one half of the value columns, so its
+// V tiles are half as large (a third ring stage fits) and its step a quarter
+// shorter; a short prompt's time is its longest unit's chain of steps.
 // Workgroup b takes unit n_units-1-b/n_hg (longest first) of head group
 // b % n_hg; the dispatcher deals workgroups to the 8 XCDs round-robin, so
 // when n_hg divides 8 each XCD serves fixed kv heads and their K/V stays in
@@ -57,22 +61,37 @@ namespace ullm {
 __device__ __forceinline__ int p16_kswz(int r) { return r & 15; }
 __device__ __forceinline__ int p16_vswz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
-template <class T, int KS, int NSTG = 4 / KS>
+// Ring stages per key stream: as many K/V stages as 160 KB holds, at most 4.
+template <int KS, int DS>
+constexpr int p16_stages() {
+    constexpr int st = 160 * 1024 / (KS * (32 * 512 + 32 * 512 / DS));
+    return st > 4 ? 4 : st;
+}
+
+template <class T, int KS, int DS, int NSTG = p16_stages<KS, DS>()>
 __global__ __launch_bounds__(512, 1) void prefill16_kernel(
     const uint16_t *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int S, int start_pos, int window, int n_head, int kv_mul, int hw,
     int n_hg, int n_units, float qscale, float *__restrict__ out, KvPages pgs) {
-    constexpr int D = 256, BN = 32, RB = D * 2, TILE = BN * RB, STAGE = 2 * TILE;
+    // DS = 2: the workgroup computes the full Q.K and softmax of its rows but
+    // P.V and the output for one half of the 256 value columns only; its V
+    // tiles hold that half (256-byte rows).
+    constexpr int D = 256, BN = 32, RB = D * 2, RBV = RB / DS;
+    constexpr int TILE = BN * RB, TILEV = BN * RBV, STAGE = TILE + TILEV;
     constexpr int NW = 8, NWS = NW / KS;  // waves per stream
-    constexpr int NIC = TILE / 1024 / NWS;                 // 1 KiB DMA chunks per wave, K or V
-    constexpr int NKS = D / 32, NDT = D / 16;
+    constexpr int NIC = TILE / 1024 / NWS;    // 1 KiB DMA chunks per wave, K
+    constexpr int NICV = TILEV / 1024 / NWS;  // and V
+    constexpr int NKS = D / 32, NDT = D / 16 / DS;  // Q k-steps; value d tiles of this workgroup
     constexpr bool CVTV = __is_same(T, BF16);
     constexpr float kLazy = 8.0f;
     static_assert(KS == 1 || KS == 2, "key streams");
-    static_assert(KS * NSTG * STAGE <= 160 * 1024, "LDS ring");
+    static_assert(DS == 1 || DS == 2, "value column split");
+    static_assert(NSTG >= 2 && KS * NSTG * STAGE <= 160 * 1024, "LDS ring");
     __shared__ __attribute__((aligned(1024))) char lds[KS * NSTG * STAGE];
 
-    const int hg = blockIdx.x % n_hg, u = n_units - 1 - (int)(blockIdx.x / n_hg);
+    const int dh = DS == 1 ? 0 : (int)(blockIdx.x % DS);  // value half
+    const int bx = (int)(blockIdx.x / DS);
+    const int hg = bx % n_hg, u = n_units - 1 - bx / n_hg;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ks = wave / NWS, ws = wave % NWS;  // key stream, wave within the stream
@@ -108,12 +127,19 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t vrs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
-    int kofs[NIC], vofs[NIC];
+    int kofs[NIC], vofs[NICV];
 #pragma unroll
     for (int i = 0; i < NIC; i++) {
         const int r = (ws * NIC + i) * 2 + (lane >> 5);
         kofs[i] = r * rbg + (((lane & 31) ^ p16_kswz(r)) * 16);
-        vofs[i] = r * rbg + (((lane & 31) ^ p16_vswz(r)) * 16);
+    }
+    // A V chunk is 1024 / RBV rows; slot c of row r takes the row's value
+    // chunk (c ^ p16_vswz(r)) of half dh.
+    constexpr int VSL = RBV / 16;  // 16-byte slots per V row
+#pragma unroll
+    for (int i = 0; i < NICV; i++) {
+        const int r = (ws * NICV + i) * (1024 / RBV) + lane / VSL;
+        vofs[i] = r * rbg + ((((lane % VSL) ^ p16_vswz(r)) + dh * 16) * 16);
     }
     char *const ring = lds + ks * NSTG * STAGE;
     auto issue = [&](int j) {  // step j's tile of this stream into stage j % NSTG
@@ -123,22 +149,23 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
         int so;
         if (pgs.tab && live) page_tile<D>(pgs, kc, vc, kvh, rbg, kv_len, t * BN, kr, vr, so);
         else so = __builtin_amdgcn_readfirstlane(live ? t * BN * rbg : range);  // range 0 if paged
-        char *st = ring + (j % NSTG) * STAGE + ws * NIC * 1024;
+        char *st = ring + (j % NSTG) * STAGE;
 #pragma unroll
-        for (int i = 0; i < NIC; i++) dma16(kr, st + i * 1024, kofs[i] + so, 0);
+        for (int i = 0; i < NIC; i++) dma16(kr, st + (ws * NIC + i) * 1024, kofs[i] + so, 0);
 #pragma unroll
-        for (int i = 0; i < NIC; i++) dma16(vr, st + TILE + i * 1024, vofs[i] + so, 0);
+        for (int i = 0; i < NICV; i++)
+            dma16(vr, st + TILE + (ws * NICV + i) * 1024, vofs[i] + so, 0);
     };
     // bf16 V -> f16 in place, for the chunks this wave's DMA wrote.
     auto widen = [&](int stg) {
         if constexpr (CVTV) {
-            const uint32_t vb = lds_addr(ring + stg * STAGE + TILE + ws * NIC * 1024) + lane * 16;
-            u32x4 w[NIC];
+            const uint32_t vb = lds_addr(ring + stg * STAGE + TILE + ws * NICV * 1024) + lane * 16;
+            u32x4 w[NICV];
 #pragma unroll
-            for (int i = 0; i < NIC; i++) w[i] = lds_read_b128(vb + i * 1024);
+            for (int i = 0; i < NICV; i++) w[i] = lds_read_b128(vb + i * 1024);
             lds_wait_any();
 #pragma unroll
-            for (int i = 0; i < NIC; i++) {
+            for (int i = 0; i < NICV; i++) {
                 tie(w[i]);
                 u32x4 o;
 #pragma unroll
@@ -156,14 +183,14 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
     for (int s = 0; s < 4; s++) ka[s] = r16 * RB + (((4 * s + g) ^ p16_kswz(r16)) * 16);
     // V^T (A operand of O^T): the 16 lanes of group g read rows 4g + r16/4
     // (+16), elements dt*16 + 4*(r16 % 4) .. +3; transposed, lane r16 gets
-    // V[4g + 0..3][dt*16 + r16].  d tiles 8.. sit 256 bytes after 0..7.
+    // V[4g + 0..3][dt*16 + r16].  d tiles 8.. sit 256 bytes after 0..7 (DS 1).
     uint32_t va[8];
     {
         const int vr = 4 * g + (r16 >> 2);
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
             const int ch = 2 * dt + ((r16 & 3) >> 1);
-            va[dt] = TILE + vr * RB + ((ch ^ p16_vswz(vr)) * 16) + 8 * (r16 & 1);
+            va[dt] = TILE + vr * RBV + ((ch ^ p16_vswz(vr)) * 16) + 8 * (r16 & 1);
         }
     }
 
@@ -202,7 +229,7 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
         auto rdv = [&](auto dtc) {
             constexpr int dt = decltype(dtc)::value;
             const u32x2 lo = lds_read_tr16_b64_at<(dt >> 3) * 256>(vaddr[dt & 7]);
-            const u32x2 hi = lds_read_tr16_b64_at<(dt >> 3) * 256 + 16 * RB>(vaddr[dt & 7]);
+            const u32x2 hi = lds_read_tr16_b64_at<(dt >> 3) * 256 + 16 * RBV>(vaddr[dt & 7]);
             vb[dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         };
         asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
@@ -260,12 +287,16 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
         asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
         static_for<0, NDT>([&](auto dc) {
             constexpr int dt = decltype(dc)::value;
-            if constexpr (dt == 4 || dt == 8) asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
-            if constexpr (dt == 12) lds_wait_any();
+            if constexpr (NDT == 16) {
+                if constexpr (dt == 4 || dt == 8) asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+                if constexpr (dt == 12) lds_wait_any();
+            } else if constexpr (dt == 4) {
+                lds_wait_any();
+            }
             tie(vb[dt]);
             oacc[dt] = mfma16<F16>(vb[dt], ph, oacc[dt]);
-            if constexpr (dt == 0) { rdv(Int<8>{}); rdv(Int<9>{}); rdv(Int<10>{}); rdv(Int<11>{}); }
-            if constexpr (dt == 4) { rdv(Int<12>{}); rdv(Int<13>{}); rdv(Int<14>{}); rdv(Int<15>{}); }
+            if constexpr (NDT == 16 && dt == 0) { rdv(Int<8>{}); rdv(Int<9>{}); rdv(Int<10>{}); rdv(Int<11>{}); }
+            if constexpr (NDT == 16 && dt == 4) { rdv(Int<12>{}); rdv(Int<13>{}); rdv(Int<14>{}); rdv(Int<15>{}); }
         });
     };
 
@@ -286,7 +317,7 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
 #pragma unroll
     for (int j = 1; j < NSTG - 1; j++) issue(j);
     for (int j = 0; j < nsteps; j++) {
-        __builtin_amdgcn_s_waitcnt(vm_wait((NSTG - 2) * 2 * NIC));
+        __builtin_amdgcn_s_waitcnt(vm_wait((NSTG - 2) * (NIC + NICV)));
 #pragma unroll
         for (int s = 0; s < NKS; s++) tie(qreg[s]);
         widen(j % NSTG);
@@ -332,7 +363,7 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
     }
     if (qrow < S) {
         const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-        float *op = out + (int64_t)qrow * q_dim + (int64_t)head * D + 4 * g;
+        float *op = out + (int64_t)qrow * q_dim + (int64_t)head * D + dh * (D / DS) + 4 * g;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++)
             __builtin_nontemporal_store(oacc[dt] * inv, (f32x4 *)(op + dt * 16));
@@ -345,34 +376,54 @@ static int p16_hw(int kv_mul, int nws) {
     return hw;
 }
 
-// Key streams for a prompt: two when whole units would leave most CUs idle.
-int prefill16_streams(int S, int n_head, int kv_mul) {
-    static const int e = env_override("ULLM_HIP_P16_KS");  // tuning override
-    if (e == 1 || e == 2) return e;
+// Key streams and value-column split for a prompt.  Two key streams when
+// whole units would leave CUs idle, or fill the chip exactly with causal
+// (window-free) chains, whose longest unit then sets the time; the value
+// split on top when the workgroups still fit one per CU.  Measured at 8/4
+// heads, f16 (us; KS/DS): S=1024 KS2/DS2 23.9, KS2/DS1 27.1, KS1/DS2 34.5;
+// S=2048 KS2/DS1 51.5, KS2/DS2 53.2; S=4096 causal KS2/DS1 122-130, KS1/DS1
+// 134-137; S=4096 window 1024 KS1/DS1 57.9, KS2/DS1 76.6; 16/8 heads at
+// S=1024 KS2/DS1 31.2, KS2/DS2 34.3.
+static void prefill16_plan(int S, int start_pos, int window, int n_head, int kv_mul, int &ks,
+                           int &ds) {
+    static const int eks = env_override("ULLM_HIP_P16_KS");  // tuning overrides
+    static const int eds = env_override("ULLM_HIP_P16_DS");
     const int hw = p16_hw(kv_mul, 8);
-    const int n_units = (S + 128 / hw - 1) / (128 / hw);
-    return (int64_t)n_units * (n_head / hw) < 256 ? 2 : 1;
+    const int64_t grid1 = (int64_t)((S + 128 / hw - 1) / (128 / hw)) * (n_head / hw);
+    const bool binding = window > 0 && window < start_pos + S;
+    ks = grid1 < 256 || (grid1 == 256 && !binding) ? 2 : 1;
+    if (eks == 1 || eks == 2) ks = eks;
+    const int hw2 = p16_hw(kv_mul, 8 / ks), ur = 16 * (8 / ks) / hw2;
+    const int64_t grid = (int64_t)((S + ur - 1) / ur) * (n_head / hw2);
+    ds = ks == 2 && grid * 2 <= 256 ? 2 : 1;
+    if (eds == 1 || eds == 2) ds = eds;
 }
 
 int launch_prefill16(int dtype, const void *q, const void *kc, const void *vc, int64_t kvs, int S,
                      int start_pos, int window, int n_head, int kv_mul, float qs, float *out,
                      hipStream_t st, KvPages pgs) {
-    const int KS = prefill16_streams(S, n_head, kv_mul);
+    int KS, DS;
+    prefill16_plan(S, start_pos, window, n_head, kv_mul, KS, DS);
     const int hw = p16_hw(kv_mul, 8 / KS), UR = 16 * (8 / KS) / hw;
     const int n_units = (S + UR - 1) / UR, n_hg = n_head / hw;
-    const dim3 grid((unsigned)(n_units * n_hg));
+    const dim3 grid((unsigned)(n_units * n_hg * DS));
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, grid, dim3(512), 0, st, (const uint16_t *)q, (const char *)kc,
                            (const char *)vc, kvs, S, start_pos, window, n_head, kv_mul, hw, n_hg,
                            n_units, qs, out, pgs);
     };
-    if (dtype == ULLM_DT_BF16) {
-        if (KS == 2) go(prefill16_kernel<BF16, 2>);
-        else go(prefill16_kernel<BF16, 1>);
-    } else {
-        if (KS == 2) go(prefill16_kernel<F16, 2>);
-        else go(prefill16_kernel<F16, 1>);
-    }
+    auto pick = [&](auto t) {
+        using T = decltype(t);
+        if (KS == 2) {
+            if (DS == 2) go(prefill16_kernel<T, 2, 2>);
+            else go(prefill16_kernel<T, 2, 1>);
+        } else {
+            if (DS == 2) go(prefill16_kernel<T, 1, 2>);
+            else go(prefill16_kernel<T, 1, 1>);
+        }
+    };
+    if (dtype == ULLM_DT_BF16) pick(BF16{});
+    else pick(F16{});
     return check_hip(hipGetLastError(), "prefill (16-row waves) launch");
 }
 
