@@ -688,6 +688,218 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
                        out, ws_ml, ws_acc);
 }
 
+// Splits of one 32-key block (short contexts: cfg2 cuts 4096 keys into 128
+// splits per kv head).  Straight-line code for the one block: q loads, the
+// block's K and V DMA, S^T = K.Q^T and the softmax once K has landed, then
+// O^T += V^T.P^T and the split's store.  CW waves may share the block: each
+// fetches 1/CW of the K and V tiles and, after a barrier, computes the full
+// Q.K and softmax (the same values in each) and P.V for its 1/CW of the d
+// tiles.  Measured at cfg2 (us per layer, graph of 28 layers): CW 1 6.44,
+// 2 6.45, 4 6.65, 8 7.31, against 6.92 for the same splits on
+// decode_dma_kernel's one-wave workgroups (its two-stage loop around the
+// one block).  Same arguments, masks and partial layout as
+// decode_dma_kernel (chunk must be 32).
+template <class T, int D, int CW>
+__global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
+    const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
+    int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
+    int fetch_len, int n_head, int kv_mul, int gt, int n_units, int chunk, int splits, float qscale,
+    float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc) {
+    constexpr int NS = D / 32;          // QK k-steps (32 d each)
+    constexpr int NDT = D / 16;         // 16-wide d tiles of O^T
+    constexpr int NDW = NDT / CW;       // d tiles per wave
+    constexpr int RB = D * 2;           // bytes per key row of one head
+    constexpr int SLOTS = D / 8;        // 16-byte slots per row
+    constexpr int RPI = 1024 / RB;      // rows written by one DMA instruction
+    constexpr int NI = kTok / RPI;      // DMA instructions per K (or V) tile
+    constexpr int NIW = NI / CW;        // ... per wave
+    constexpr int TILE = kTok * RB;
+    constexpr bool SPLITP = __is_same(T, BF16);
+    static_assert(D == 64 || D == 128, "head_dim 64 and 128");
+    static_assert(NIW >= 1 && NDW >= 1, "quarter tiles");
+
+    const int split = blockIdx.x, unit = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n16 = lane & 15, kg = lane >> 4;
+    const int head0 = unit * gt, kvh = head0 / kv_mul;
+    const bool head_ok = n16 < gt;
+    __shared__ __attribute__((aligned(1024))) char lds[2 * TILE];  // K tile, then V tile
+
+    // Length, window start and fetched range exactly as decode_dma_kernel.
+    const __amdgpu_buffer_rsrc_t lrs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(seq_lens + b), 0, 4, kRsrcWord3);
+    int lenv = __builtin_amdgcn_raw_buffer_load_b32(lrs, 0, 0, 0);
+    int len;
+    auto take_len = [&] {
+        asm volatile("" : "+v"(lenv));
+        len = __builtin_amdgcn_readfirstlane(lenv);
+    };
+    if (fetch_len <= 0) take_len();
+    const int start = (fetch_len > 0 || window <= 0 || len <= window) ? 0 : len - window;
+    const int c0 = (fetch_len > 0 ? 0 : start) + split * chunk;
+    const int cf = fetch_len > 0 ? min(c0 + chunk, fetch_len) : min(c0 + chunk, len);
+
+    const int rb = (int)(kv_stride * 2);
+    const char *kb0 = kc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
+    const char *vb0 = vc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
+    const int range = cf > 0 ? (cf - 1) * rb + D * 2 : 0;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kb0), 0, range, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vb0), 0, range, kRsrcWord3);
+
+    // q first, then this wave's DMA instructions of the K tile, then of V.
+    f32x4 qa[NS][2];
+    {
+        const float *qp = q + ((int64_t)b * n_head + head0 + (head_ok ? n16 : 0)) * D;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            qa[s][0] = *(const f32x4 *)(qp + (s * 4 + kg) * 8);
+            qa[s][1] = *(const f32x4 *)(qp + (s * 4 + kg) * 8 + 4);
+        }
+    }
+    const bool any = c0 < cf;  // workgroup-uniform
+    if (any) {
+        const int so = __builtin_amdgcn_readfirstlane(c0 * rb);
+        const int drow = lane / SLOTS, dslot = lane % SLOTS;
+#pragma unroll
+        for (int i = 0; i < NIW; i++) {
+            const int r = (wave * NIW + i) * RPI + drow;
+            dma16(krs, lds + (wave * NIW + i) * 1024, r * rb + ((dslot ^ (r & (SLOTS - 1))) * 16) + so, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < NIW; i++) {
+            const int r = (wave * NIW + i) * RPI + drow;
+            dma16(vrs, lds + TILE + (wave * NIW + i) * 1024,
+                  r * rb + ((dslot ^ (r & (SLOTS - 1))) * 16) + so, 0);
+        }
+    }
+    if (fetch_len > 0) take_len();
+    const int c1 = min(c0 + chunk, len);
+
+    u32x4 qh[NS], ql[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float x0 = head_ok ? qa[s][j >> 1][(2 * j) & 3] * qscale : 0.f;
+            const float x1 = head_ok ? qa[s][j >> 1][(2 * j + 1) & 3] * qscale : 0.f;
+            const u32x2 hl = split2<T>(x0, x1);
+            qh[s][j] = hl[0];
+            ql[s][j] = hl[1];
+        }
+
+    f32x4 oacc[NDW];
+#pragma unroll
+    for (int i = 0; i < NDW; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_part = 0.f;
+    if (any) {
+        // K: this wave's part landed (V still counted), then every wave's.
+        __builtin_amdgcn_s_waitcnt(vm_wait(NIW));
+        if constexpr (CW > 1) __syncthreads();
+        const int tb = c0;
+        if (tb < c1) {
+            const uint32_t kbase = lds_addr(lds);
+            u32x4 ka[2 * NS];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int r = t * 16 + n16;
+#pragma unroll
+                for (int s = 0; s < NS; s++)
+                    ka[t * NS + s] = lds_read_b128(kbase + r * RB + (((s * 4 + kg) ^ (r & (SLOTS - 1))) * 16));
+            }
+            lds_wait(ka);
+            f32x4 sacc[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < NS; s++) {
+                    sacc[t] = mfma16<T>(ka[t * NS + s], qh[s], sacc[t]);
+                    sacc[t] = mfma16<T>(ka[t * NS + s], ql[s], sacc[t]);
+                }
+            }
+            float sv[8];
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) sv[t * 4 + i] = sacc[t][i];
+            if (tb + kTok > c1) {
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (tb + t * 16 + kg * 4 + i >= c1) sv[t * 4 + i] = -INFINITY;
+            }
+            float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                             fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+            m_run = rows_max(mt);
+            const float mu = m_run == -INFINITY ? 0.f : m_run;
+            float p[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) { p[i] = __builtin_amdgcn_exp2f(sv[i] - mu); l_part += p[i]; }
+            u32x4 ph, pl;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if constexpr (SPLITP) {
+                    const u32x2 hl = split2<T>(p[2 * j], p[2 * j + 1]);
+                    ph[j] = hl[0];
+                    pl[j] = hl[1];
+                } else {
+                    ph[j] = pack2<T>(p[2 * j], p[2 * j + 1]);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(vm_wait(0));
+            if constexpr (CW > 1) __syncthreads();
+            const uint32_t vbase = lds_addr(lds + TILE);
+            if (tb + kTok > c1) {
+                // Fetched rows at or past the length hold whatever the cache
+                // holds there (P is 0 for them, but 0 * NaN is NaN): each
+                // wave zeroes them before its own reads (the same zeros).
+                const int nv = max(c1 - tb, 0);
+                for (int i = nv * SLOTS + lane; i < kTok * SLOTS; i += 64)
+                    lds_write_b128(vbase + i * 16, u32x4{0u, 0u, 0u, 0u});
+            }
+            const int vr0 = kg * 4 + (n16 >> 2);
+            u32x4 va[NDW];
+#pragma unroll
+            for (int i = 0; i < NDW; i++) {
+                const int dt = wave * NDW + i;
+                const int ch = dt * 2 + ((n16 & 3) >> 1);
+                const int bo = 8 * (n16 & 1);
+                const u32x2 l2 = lds_read_tr16_b64(vbase + vr0 * RB + ((ch ^ (vr0 & (SLOTS - 1))) * 16) + bo);
+                const u32x2 h2 = lds_read_tr16_b64(vbase + (vr0 + 16) * RB +
+                                                   ((ch ^ ((vr0 + 16) & (SLOTS - 1))) * 16) + bo);
+                va[i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+            }
+            lds_wait(va);
+#pragma unroll
+            for (int i = 0; i < NDW; i++) {
+                oacc[i] = mfma16<T>(va[i], ph, oacc[i]);
+                if constexpr (SPLITP) oacc[i] = mfma16<T>(va[i], pl, oacc[i]);
+            }
+        } else {
+            __builtin_amdgcn_s_waitcnt(vm_wait(0));
+        }
+    }
+    l_part = rows_sum(l_part);
+    if (!head_ok) return;
+    const int64_t u = (int64_t)b * n_units + unit;
+    if (splits == 1) {
+#pragma unroll
+        for (int i = 0; i < NDW; i++)
+            store_split<D>(oacc[i], m_run, l_part, (wave * NDW + i) * 4 + kg, n16, b, split, splits,
+                           gt, n_head, head0, u, gt * D, out, ws_ml, ws_acc);
+    } else {
+        float *ap = ws_acc + (u * splits + split) * (gt * D) + n16 * D + kg * 4;
+#pragma unroll
+        for (int i = 0; i < NDW; i++) *(f32x4 *)(ap + (wave * NDW + i) * 16) = oacc[i];
+        if (wave == 0 && kg == 0)
+            *(float2 *)(ws_ml + ((u * splits + split) * gt + n16) * 2) = float2{m_run, l_part};
+    }
+}
+
 constexpr int kMaxSplits = 256;
 
 // Combines the split partials of one (sequence, head) in one round trip.
@@ -789,6 +1001,11 @@ struct MfmaPlan {
 
 static const int kEnvMw = env_override("ULLM_HIP_DECODE_MW");
 static const int kEnvSplitsM = env_override("ULLM_HIP_DECODE_SPLITS");
+// Tuning overrides: ULLM_HIP_DECODE_NOBLOCK=1 runs one-block splits on
+// decode_dma_kernel instead of decode_block_kernel; ULLM_HIP_DECODE_CW=2/4
+// shares each block among that many waves.
+static const bool kNoBlock = env_override("ULLM_HIP_DECODE_NOBLOCK") == 1;
+static const int kEnvCw = env_override("ULLM_HIP_DECODE_CW");
 
 static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_len, int window) {
     MfmaPlan p{};
@@ -932,6 +1149,21 @@ static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const
     // Keys 0..max_len-1 of every sequence are readable (the cache holds them);
     // when the window cannot bind, the kernels fetch keys before the length.
     const int fetch_len = (win <= 0 || max_len <= win) ? max_len : 0;
+    if constexpr (D <= 128) {
+        if (p.mw == 1 && p.chunk == kTok && p.splits > 1 && !kNoBlock) {
+            auto go = [&](auto kern, int cw) {
+                hipLaunchKernelGGL(kern, dim3(p.splits, p.n_units, batch), dim3(cw * 64), 0, st, q, (const char *)kc, (const char *)vc, kvs, ss,
+                               lens, win, fetch_len, nh, kv_mul, p.gt, p.n_units, p.chunk,
+                               p.splits, qs, out, (float *)(ws + p.off_ml),
+                               (float *)(ws + p.off_acc));
+            };
+            if (kEnvCw == 2) go(decode_block_kernel<T, D, 2>, 2);
+            else if (kEnvCw == 4) go(decode_block_kernel<T, D, 4>, 4);
+            else go(decode_block_kernel<T, D, 1>, 1);
+            launch_merge<D>(p, batch, nh, out, ws, st);
+            return;
+        }
+    }
     MainLaunch<T, D>::run(p.mw, dim3(p.splits, p.n_units, batch), st, q, (const char *)kc,
                           (const char *)vc, kvs, ss, lens, win, fetch_len, nh, kv_mul, p.gt,
                           p.n_units,
