@@ -699,7 +699,7 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
 // decode_dma_kernel's one-wave workgroups (its two-stage loop around the
 // one block).  Same arguments, masks and partial layout as
 // decode_dma_kernel (chunk must be 32).
-template <class T, int D, int CW>
+template <class T, int D, int CW, int NB>
 __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
@@ -724,7 +724,8 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
     const int n16 = lane & 15, kg = lane >> 4;
     const int head0 = unit * gt, kvh = head0 / kv_mul;
     const bool head_ok = n16 < gt;
-    __shared__ __attribute__((aligned(1024))) char lds[2 * TILE];  // K tile, then V tile
+    // Block i: K tile at 2i TILE, V tile at (2i + 1) TILE.
+    __shared__ __attribute__((aligned(1024))) char lds[2 * NB * TILE];
 
     // Length, window start and fetched range exactly as decode_dma_kernel.
     const __amdgpu_buffer_rsrc_t lrs =
@@ -749,7 +750,8 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
     const __amdgpu_buffer_rsrc_t vrs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vb0), 0, range, kRsrcWord3);
 
-    // q first, then this wave's DMA instructions of the K tile, then of V.
+    // q first, then this wave's DMA instructions of every block: K0, V0, K1, ...
+    // (a block wholly past the fetched range is not requested).
     f32x4 qa[NS][2];
     {
         const float *qp = q + ((int64_t)b * n_head + head0 + (head_ok ? n16 : 0)) * D;
@@ -759,21 +761,27 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             qa[s][1] = *(const f32x4 *)(qp + (s * 4 + kg) * 8 + 4);
         }
     }
-    const bool any = c0 < cf;  // workgroup-uniform
-    if (any) {
-        const int so = __builtin_amdgcn_readfirstlane(c0 * rb);
+    const int nfb = min(max((cf - c0 + kTok - 1) / kTok, 0), NB);  // blocks fetched (uniform)
+    {
         const int drow = lane / SLOTS, dslot = lane % SLOTS;
+        static_for<0, NB>([&](auto bc) {
+            constexpr int bi = decltype(bc)::value;
+            if (bi < nfb) {
+                const int so = __builtin_amdgcn_readfirstlane((c0 + bi * kTok) * rb);
 #pragma unroll
-        for (int i = 0; i < NIW; i++) {
-            const int r = (wave * NIW + i) * RPI + drow;
-            dma16(krs, lds + (wave * NIW + i) * 1024, r * rb + ((dslot ^ (r & (SLOTS - 1))) * 16) + so, 0);
-        }
+                for (int i = 0; i < NIW; i++) {
+                    const int r = (wave * NIW + i) * RPI + drow;
+                    dma16(krs, lds + 2 * bi * TILE + (wave * NIW + i) * 1024,
+                          r * rb + ((dslot ^ (r & (SLOTS - 1))) * 16) + so, 0);
+                }
 #pragma unroll
-        for (int i = 0; i < NIW; i++) {
-            const int r = (wave * NIW + i) * RPI + drow;
-            dma16(vrs, lds + TILE + (wave * NIW + i) * 1024,
-                  r * rb + ((dslot ^ (r & (SLOTS - 1))) * 16) + so, 0);
-        }
+                for (int i = 0; i < NIW; i++) {
+                    const int r = (wave * NIW + i) * RPI + drow;
+                    dma16(vrs, lds + (2 * bi + 1) * TILE + (wave * NIW + i) * 1024,
+                          r * rb + ((dslot ^ (r & (SLOTS - 1))) * 16) + so, 0);
+                }
+            }
+        });
     }
     if (fetch_len > 0) take_len();
     const int c1 = min(c0 + chunk, len);
@@ -794,95 +802,111 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
 #pragma unroll
     for (int i = 0; i < NDW; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_part = 0.f;
-    if (any) {
-        // K: this wave's part landed (V still counted), then every wave's.
-        __builtin_amdgcn_s_waitcnt(vm_wait(NIW));
+    // Block bi: its K is waited for with V bi and the later blocks still
+    // counted; its V with the later blocks counted.  Those counts hold when
+    // every block was fetched; a split with fewer (the end of a sequence)
+    // waits for all of its DMA instead.
+    static_for<0, NB>([&](auto bc) {
+        constexpr int bi = decltype(bc)::value;
+        const int tb = c0 + bi * kTok;
+        if (bi >= nfb) return;
+        if (nfb == NB) __builtin_amdgcn_s_waitcnt(vm_wait((2 * (NB - bi) - 1) * NIW));
+        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
         if constexpr (CW > 1) __syncthreads();
-        const int tb = c0;
-        if (tb < c1) {
-            const uint32_t kbase = lds_addr(lds);
-            u32x4 ka[2 * NS];
+        if (tb >= c1) {  // fetched but past the length: nothing to add
+            __builtin_amdgcn_s_waitcnt(vm_wait(0));
+            return;
+        }
+        const uint32_t kbase = lds_addr(lds + 2 * bi * TILE);
+        u32x4 ka[2 * NS];
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const int r = t * 16 + n16;
+        for (int t = 0; t < 2; t++) {
+            const int r = t * 16 + n16;
 #pragma unroll
-                for (int s = 0; s < NS; s++)
-                    ka[t * NS + s] = lds_read_b128(kbase + r * RB + (((s * 4 + kg) ^ (r & (SLOTS - 1))) * 16));
+            for (int s = 0; s < NS; s++)
+                ka[t * NS + s] = lds_read_b128(kbase + r * RB + (((s * 4 + kg) ^ (r & (SLOTS - 1))) * 16));
+        }
+        lds_wait(ka);
+        f32x4 sacc[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                sacc[t] = mfma16<T>(ka[t * NS + s], qh[s], sacc[t]);
+                sacc[t] = mfma16<T>(ka[t * NS + s], ql[s], sacc[t]);
             }
-            lds_wait(ka);
-            f32x4 sacc[2];
+        }
+        float sv[8];
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int s = 0; s < NS; s++) {
-                    sacc[t] = mfma16<T>(ka[t * NS + s], qh[s], sacc[t]);
-                    sacc[t] = mfma16<T>(ka[t * NS + s], ql[s], sacc[t]);
-                }
-            }
-            float sv[8];
+            for (int i = 0; i < 4; i++) sv[t * 4 + i] = sacc[t][i];
+        if (tb + kTok > c1) {
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) sv[t * 4 + i] = sacc[t][i];
-            if (tb + kTok > c1) {
-#pragma unroll
-                for (int t = 0; t < 2; t++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        if (tb + t * 16 + kg * 4 + i >= c1) sv[t * 4 + i] = -INFINITY;
-            }
-            float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                             fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-            m_run = rows_max(mt);
-            const float mu = m_run == -INFINITY ? 0.f : m_run;
-            float p[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) { p[i] = __builtin_amdgcn_exp2f(sv[i] - mu); l_part += p[i]; }
-            u32x4 ph, pl;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if constexpr (SPLITP) {
-                    const u32x2 hl = split2<T>(p[2 * j], p[2 * j + 1]);
-                    ph[j] = hl[0];
-                    pl[j] = hl[1];
-                } else {
-                    ph[j] = pack2<T>(p[2 * j], p[2 * j + 1]);
-                }
-            }
-            __builtin_amdgcn_s_waitcnt(vm_wait(0));
-            if constexpr (CW > 1) __syncthreads();
-            const uint32_t vbase = lds_addr(lds + TILE);
-            if (tb + kTok > c1) {
-                // Fetched rows at or past the length hold whatever the cache
-                // holds there (P is 0 for them, but 0 * NaN is NaN): each
-                // wave zeroes them before its own reads (the same zeros).
-                const int nv = max(c1 - tb, 0);
-                for (int i = nv * SLOTS + lane; i < kTok * SLOTS; i += 64)
-                    lds_write_b128(vbase + i * 16, u32x4{0u, 0u, 0u, 0u});
-            }
-            const int vr0 = kg * 4 + (n16 >> 2);
-            u32x4 va[NDW];
-#pragma unroll
-            for (int i = 0; i < NDW; i++) {
-                const int dt = wave * NDW + i;
-                const int ch = dt * 2 + ((n16 & 3) >> 1);
-                const int bo = 8 * (n16 & 1);
-                const u32x2 l2 = lds_read_tr16_b64(vbase + vr0 * RB + ((ch ^ (vr0 & (SLOTS - 1))) * 16) + bo);
-                const u32x2 h2 = lds_read_tr16_b64(vbase + (vr0 + 16) * RB +
-                                                   ((ch ^ ((vr0 + 16) & (SLOTS - 1))) * 16) + bo);
-                va[i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
-            }
-            lds_wait(va);
-#pragma unroll
-            for (int i = 0; i < NDW; i++) {
-                oacc[i] = mfma16<T>(va[i], ph, oacc[i]);
-                if constexpr (SPLITP) oacc[i] = mfma16<T>(va[i], pl, oacc[i]);
-            }
-        } else {
-            __builtin_amdgcn_s_waitcnt(vm_wait(0));
+                for (int i = 0; i < 4; i++)
+                    if (tb + t * 16 + kg * 4 + i >= c1) sv[t * 4 + i] = -INFINITY;
         }
-    }
+        float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                         fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+        mt = rows_max(mt);
+        const float m_new = fmaxf(m_run, mt);
+        const float mu = m_new == -INFINITY ? 0.f : m_new;
+        if (bi > 0 && __any(m_new != m_run)) {
+            const float corr = __builtin_amdgcn_exp2f(m_run - mu);
+            l_part *= corr;
+#pragma unroll
+            for (int i = 0; i < NDW; i++) oacc[i] *= corr;
+        }
+        m_run = m_new;
+        float p[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) { p[i] = __builtin_amdgcn_exp2f(sv[i] - mu); l_part += p[i]; }
+        u32x4 ph, pl;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if constexpr (SPLITP) {
+                const u32x2 hl = split2<T>(p[2 * j], p[2 * j + 1]);
+                ph[j] = hl[0];
+                pl[j] = hl[1];
+            } else {
+                ph[j] = pack2<T>(p[2 * j], p[2 * j + 1]);
+            }
+        }
+        if (nfb == NB) __builtin_amdgcn_s_waitcnt(vm_wait(2 * (NB - bi - 1) * NIW));
+        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
+        if constexpr (CW > 1) __syncthreads();
+        const uint32_t vbase = lds_addr(lds + (2 * bi + 1) * TILE);
+        if (tb + kTok > c1) {
+            // Fetched rows at or past the length hold whatever the cache
+            // holds there (P is 0 for them, but 0 * NaN is NaN): each
+            // wave zeroes them before its own reads (the same zeros).
+            const int nv = max(c1 - tb, 0);
+            for (int i = nv * SLOTS + lane; i < kTok * SLOTS; i += 64)
+                lds_write_b128(vbase + i * 16, u32x4{0u, 0u, 0u, 0u});
+        }
+        const int vr0 = kg * 4 + (n16 >> 2);
+        u32x4 va[NDW];
+#pragma unroll
+        for (int i = 0; i < NDW; i++) {
+            const int dt = wave * NDW + i;
+            const int ch = dt * 2 + ((n16 & 3) >> 1);
+            const int bo = 8 * (n16 & 1);
+            const u32x2 l2 = lds_read_tr16_b64(vbase + vr0 * RB + ((ch ^ (vr0 & (SLOTS - 1))) * 16) + bo);
+            const u32x2 h2 = lds_read_tr16_b64(vbase + (vr0 + 16) * RB +
+                                               ((ch ^ ((vr0 + 16) & (SLOTS - 1))) * 16) + bo);
+            va[i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+        }
+        lds_wait(va);
+#pragma unroll
+        for (int i = 0; i < NDW; i++) {
+            oacc[i] = mfma16<T>(va[i], ph, oacc[i]);
+            if constexpr (SPLITP) oacc[i] = mfma16<T>(va[i], pl, oacc[i]);
+        }
+    });
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));  // no DMA may outlive the workgroup
     l_part = rows_sum(l_part);
     if (!head_ok) return;
     const int64_t u = (int64_t)b * n_units + unit;
@@ -1150,16 +1174,17 @@ static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const
     // when the window cannot bind, the kernels fetch keys before the length.
     const int fetch_len = (win <= 0 || max_len <= win) ? max_len : 0;
     if constexpr (D <= 128) {
-        if (p.mw == 1 && p.chunk == kTok && p.splits > 1 && !kNoBlock) {
+        if (p.mw == 1 && (p.chunk == kTok || p.chunk == 2 * kTok) && p.splits > 1 && !kNoBlock) {
             auto go = [&](auto kern, int cw) {
                 hipLaunchKernelGGL(kern, dim3(p.splits, p.n_units, batch), dim3(cw * 64), 0, st, q, (const char *)kc, (const char *)vc, kvs, ss,
                                lens, win, fetch_len, nh, kv_mul, p.gt, p.n_units, p.chunk,
                                p.splits, qs, out, (float *)(ws + p.off_ml),
                                (float *)(ws + p.off_acc));
             };
-            if (kEnvCw == 2) go(decode_block_kernel<T, D, 2>, 2);
-            else if (kEnvCw == 4) go(decode_block_kernel<T, D, 4>, 4);
-            else go(decode_block_kernel<T, D, 1>, 1);
+            if (p.chunk == 2 * kTok) go(decode_block_kernel<T, D, 1, 2>, 1);
+            else if (kEnvCw == 2) go(decode_block_kernel<T, D, 2, 1>, 2);
+            else if (kEnvCw == 4) go(decode_block_kernel<T, D, 4, 1>, 4);
+            else go(decode_block_kernel<T, D, 1, 1>, 1);
             launch_merge<D>(p, batch, nh, out, ws, st);
             return;
         }
