@@ -698,8 +698,10 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
 // 2 6.45, 4 6.65, 8 7.31, against 6.92 for the same splits on
 // decode_dma_kernel's one-wave workgroups (its two-stage loop around the
 // one block).  Same arguments, masks and partial layout as
-// decode_dma_kernel (chunk must be 32).
-template <class T, int D, int CW, int NB>
+// decode_dma_kernel (chunk = NB * KB).  KB = 16 (head_dim 256): a block is one
+// 16-key tile, so a short context spreads over twice the workgroups; the
+// P^T operand's keys 16-31 are zero.
+template <class T, int D, int CW, int NB, int KB = kTok>
 __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
@@ -711,11 +713,13 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
     constexpr int RB = D * 2;           // bytes per key row of one head
     constexpr int SLOTS = D / 8;        // 16-byte slots per row
     constexpr int RPI = 1024 / RB;      // rows written by one DMA instruction
-    constexpr int NI = kTok / RPI;      // DMA instructions per K (or V) tile
+    constexpr int NI = KB / RPI;        // DMA instructions per K (or V) tile
     constexpr int NIW = NI / CW;        // ... per wave
-    constexpr int TILE = kTok * RB;
+    constexpr int TILE = KB * RB;
+    constexpr int NT = KB / 16;         // 16-key tiles per block
     constexpr bool SPLITP = __is_same(T, BF16);
-    static_assert(D == 64 || D == 128, "head_dim 64 and 128");
+    static_assert(D == 64 || D == 128 || D == 256, "head_dim 64, 128, 256");
+    static_assert(KB == 16 || KB == 32, "keys per block");
     static_assert(NIW >= 1 && NDW >= 1, "quarter tiles");
 
     const int split = blockIdx.x, unit = blockIdx.y, b = blockIdx.z;
@@ -761,13 +765,13 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             qa[s][1] = *(const f32x4 *)(qp + (s * 4 + kg) * 8 + 4);
         }
     }
-    const int nfb = min(max((cf - c0 + kTok - 1) / kTok, 0), NB);  // blocks fetched (uniform)
+    const int nfb = min(max((cf - c0 + KB - 1) / KB, 0), NB);  // blocks fetched (uniform)
     {
         const int drow = lane / SLOTS, dslot = lane % SLOTS;
         static_for<0, NB>([&](auto bc) {
             constexpr int bi = decltype(bc)::value;
             if (bi < nfb) {
-                const int so = __builtin_amdgcn_readfirstlane((c0 + bi * kTok) * rb);
+                const int so = __builtin_amdgcn_readfirstlane((c0 + bi * KB) * rb);
 #pragma unroll
                 for (int i = 0; i < NIW; i++) {
                     const int r = (wave * NIW + i) * RPI + drow;
@@ -808,7 +812,7 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
     // waits for all of its DMA instead.
     static_for<0, NB>([&](auto bc) {
         constexpr int bi = decltype(bc)::value;
-        const int tb = c0 + bi * kTok;
+        const int tb = c0 + bi * KB;
         if (bi >= nfb) return;
         if (nfb == NB) __builtin_amdgcn_s_waitcnt(vm_wait((2 * (NB - bi) - 1) * NIW));
         else __builtin_amdgcn_s_waitcnt(vm_wait(0));
@@ -818,9 +822,9 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             return;
         }
         const uint32_t kbase = lds_addr(lds + 2 * bi * TILE);
-        u32x4 ka[2 * NS];
+        u32x4 ka[NT * NS];
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
+        for (int t = 0; t < NT; t++) {
             const int r = t * 16 + n16;
 #pragma unroll
             for (int s = 0; s < NS; s++)
@@ -828,8 +832,9 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
         }
         lds_wait(ka);
         f32x4 sacc[2];
+        sacc[1] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // keys 16-31 of a 16-key block
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
+        for (int t = 0; t < NT; t++) {
             sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < NS; s++) {
@@ -842,9 +847,9 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) sv[t * 4 + i] = sacc[t][i];
-        if (tb + kTok > c1) {
+        if (tb + KB > c1) {
 #pragma unroll
-            for (int t = 0; t < 2; t++)
+            for (int t = 0; t < NT; t++)
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     if (tb + t * 16 + kg * 4 + i >= c1) sv[t * 4 + i] = -INFINITY;
@@ -879,12 +884,12 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
         else __builtin_amdgcn_s_waitcnt(vm_wait(0));
         if constexpr (CW > 1) __syncthreads();
         const uint32_t vbase = lds_addr(lds + (2 * bi + 1) * TILE);
-        if (tb + kTok > c1) {
+        if (tb + KB > c1) {
             // Fetched rows at or past the length hold whatever the cache
             // holds there (P is 0 for them, but 0 * NaN is NaN): each
             // wave zeroes them before its own reads (the same zeros).
             const int nv = max(c1 - tb, 0);
-            for (int i = nv * SLOTS + lane; i < kTok * SLOTS; i += 64)
+            for (int i = nv * SLOTS + lane; i < KB * SLOTS; i += 64)
                 lds_write_b128(vbase + i * 16, u32x4{0u, 0u, 0u, 0u});
         }
         const int vr0 = kg * 4 + (n16 >> 2);
@@ -895,9 +900,13 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             const int ch = dt * 2 + ((n16 & 3) >> 1);
             const int bo = 8 * (n16 & 1);
             const u32x2 l2 = lds_read_tr16_b64(vbase + vr0 * RB + ((ch ^ (vr0 & (SLOTS - 1))) * 16) + bo);
-            const u32x2 h2 = lds_read_tr16_b64(vbase + (vr0 + 16) * RB +
-                                               ((ch ^ ((vr0 + 16) & (SLOTS - 1))) * 16) + bo);
-            va[i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+            if constexpr (NT == 2) {
+                const u32x2 h2 = lds_read_tr16_b64(vbase + (vr0 + 16) * RB +
+                                                   ((ch ^ ((vr0 + 16) & (SLOTS - 1))) * 16) + bo);
+                va[i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+            } else {
+                va[i] = u32x4{l2[0], l2[1], 0u, 0u};  // keys 16-31 absent (P is 0 there)
+            }
         }
         lds_wait(va);
 #pragma unroll
@@ -1020,6 +1029,7 @@ namespace ullm {
 
 struct MfmaPlan {
     int gt, n_units, chunk, splits, mw;
+    int kb;  // 16: head_dim-256 splits of one 16-key block on decode_block_kernel (else 0)
     size_t off_ml, off_acc, bytes;
 };
 
@@ -1031,7 +1041,8 @@ static const int kEnvSplitsM = env_override("ULLM_HIP_DECODE_SPLITS");
 static const bool kNoBlock = env_override("ULLM_HIP_DECODE_NOBLOCK") == 1;
 static const int kEnvCw = env_override("ULLM_HIP_DECODE_CW");
 
-static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_len, int window) {
+static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_len, int window,
+                          bool paged = false) {
     MfmaPlan p{};
     const int kv_mul = n_head / n_kv_head;
     p.gt = kv_mul;
@@ -1072,6 +1083,15 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     // other three waves of a 4-wave one would have no keys).
     if (D > 128 && p.mw == kMW && splits > 1 && (chunk == kTok || kEnvMw == 1)) p.mw = 1;
     p.splits = (visible + chunk - 1) / chunk;
+    // head_dim 256, contiguous cache, one-block splits that leave CUs idle:
+    // 16-key splits on decode_block_kernel, twice the workgroups (cfg4's
+    // 1024-key window: 128 -> 256 workgroups).
+    if (D > 128 && !paged && p.mw == 1 && chunk == kTok && p.splits > 1 &&
+        units * p.splits < kMfmaTargetWG && 2 * p.splits <= kMaxSplits && !kNoBlock) {
+        p.kb = 16;
+        p.chunk = 16;
+        p.splits = (visible + 15) / 16;
+    }
     const size_t ml = ((size_t)units * p.splits * p.gt * 2 * 4 + 255) / 256 * 256;
     const size_t ac = (size_t)units * p.splits * p.gt * D * 4;
     p.off_ml = 0;
@@ -1082,14 +1102,16 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
 
 // Upper bound over every call with max_len' <= max_len (the planner's split
 // count is not monotonic in the length: short contexts use more, smaller
-// splits): every split holds at least one 32-key block, at most kMaxSplits
-// exist, and contexts of at most kMW * 4 blocks use one split.
+// splits): every split holds at least one 32-key block (16 keys at
+// head_dim 256), at most kMaxSplits exist, and contexts of at most kMW * 4
+// blocks use one split.
 size_t decode_mfma_workspace(int batch, int n_head, int n_kv_head, int D, int max_len,
                              int window) {
     const MfmaPlan p = plan_mfma(batch, n_head, n_kv_head, D, max_len, window);
     const int visible = (window > 0 && max_len > window) ? window : max_len;
     const int blocks = (visible + kTok - 1) / kTok;
-    const int smax = blocks <= kMW * 4 ? 1 : std::min(kMaxSplits, blocks);  // as plan_mfma
+    // head_dim 256 may split down to 16-key blocks.
+    const int smax = blocks <= kMW * 4 ? 1 : std::min(kMaxSplits, D > 128 ? 2 * blocks : blocks);
     if (smax <= 1) return 0;
     const size_t units = (size_t)batch * p.n_units;
     const size_t ml = (units * smax * p.gt * 2 * 4 + 255) / 256 * 256;
@@ -1173,7 +1195,16 @@ static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const
     // Keys 0..max_len-1 of every sequence are readable (the cache holds them);
     // when the window cannot bind, the kernels fetch keys before the length.
     const int fetch_len = (win <= 0 || max_len <= win) ? max_len : 0;
-    if constexpr (D <= 128) {
+    if constexpr (D > 128) {
+        if (p.kb == 16) {
+            hipLaunchKernelGGL((decode_block_kernel<T, D, 1, 1, 16>), dim3(p.splits, p.n_units, batch),
+                               dim3(64), 0, st, q, (const char *)kc, (const char *)vc, kvs, ss, lens,
+                               win, fetch_len, nh, kv_mul, p.gt, p.n_units, p.chunk, p.splits, qs,
+                               out, (float *)(ws + p.off_ml), (float *)(ws + p.off_acc));
+            launch_merge<D>(p, batch, nh, out, ws, st);
+            return;
+        }
+    } else {
         if (p.mw == 1 && (p.chunk == kTok || p.chunk == 2 * kTok) && p.splits > 1 && !kNoBlock) {
             auto go = [&](auto kern, int cw) {
                 hipLaunchKernelGGL(kern, dim3(p.splits, p.n_units, batch), dim3(cw * 64), 0, st, q, (const char *)kc, (const char *)vc, kvs, ss,
@@ -1327,7 +1358,8 @@ extern "C" int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, c
                                 __builtin_ctz(page_size), n_pages, seq_lens, max_len, window,
                                 batch, n_head, n_kv_head, head_dim, scale * kLog2e, out, workspace,
                                 workspace_bytes, (hipStream_t)stream);
-    const MfmaPlan p = plan_mfma(batch, n_head, n_kv_head, head_dim, max_len, paged_plan_window(window));
+    const MfmaPlan p = plan_mfma(batch, n_head, n_kv_head, head_dim, max_len, paged_plan_window(window),
+                                 true);
     if (p.bytes > 0 && (!workspace || workspace_bytes < p.bytes))
         return set_error(ULLM_HIP_E_WORKSPACE, "decode_paged: workspace of %zu bytes needed, %zu given",
                          p.bytes, workspace_bytes);
