@@ -694,7 +694,8 @@ def main():
                                     "256, f16 KV, context 8192; 6 layers per step = 5 sliding-"
                                     "window layers (1024 keys) + 1 global layer, rotated past "
                                     "the MALL",
-                        "kernel": "decode_mfma_kernel<F16,256> + decode_merge_kernel",
+                        "kernel": "window layers decode_block_kernel<F16,256,1,1,16>, global layer "
+                                  "decode_mfma_kernel<F16,256,false,4>; each + decode_merge_kernel",
                         "us_per_group": round(c4["ms_per_step"] * 1e3, 3),
                         "us_per_layer": round(c4["us_per_layer"], 3),
                         "algorithmic_bytes_per_group": int(c4["step_bytes"]),
@@ -772,7 +773,7 @@ def main():
                      "frac": round(d["gbps_step"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("bytes_per_launch") if traffic else None,
                      "traffic_measured_at": traffic.get("commit") if traffic else None,
-                     "kernel": "decode_dma_kernel<F16,128,1> + decode_merge_kernel<128,4,2,256> "
+                     "kernel": "decode_block_kernel<F16,128,1,1> + decode_merge_kernel<128,4,2,256> "
                                "(one decode-attention op per layer)",
                      "algorithmic_bytes": int(d["layer_bytes"]),
                      "us_per_launch": round(d["us_per_layer"], 3),
