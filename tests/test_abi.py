@@ -95,7 +95,8 @@ def test_prefill_and_append_validation():
 def test_workspace_size_planning():
     ws = L.lib().ullm_hip_decode_workspace_bytes
     assert ws(1, 12, 2, 128, 4096, 0) > 0
-    assert ws(1, 12, 2, 128, 64, 0) == 0  # one split: no partials
+    assert ws(1, 12, 2, 128, 64, 0) > 0  # a short context still splits over the CUs
+    assert ws(128, 12, 2, 128, 64, 0) == 0  # 256 units fill the chip: one split each
     assert ws(1, 32, 4, 128, 32768, 0) >= ws(1, 32, 4, 128, 4096, 0)
     assert ws(1, 12, 5, 128, 4096, 0) == 0  # invalid shape
 

@@ -1055,11 +1055,15 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     // workgroup over every CU (a CU's outstanding misses, not the waves,
     // bound how fast it streams).
     // A context of at most kMW * 4 blocks stays in one 4-wave workgroup per
-    // unit: no partials, no merge kernel.
+    // unit (no partials, no merge kernel) only when the units alone fill the
+    // chip; otherwise it is split like a long one.  Measured at 512 keys,
+    // batch 1 (us per layer, one workgroup per unit -> 16 splits): 32/8 heads
+    // D64 7.34 -> 5.46, 12/2 D128 9.81 -> 5.79, 8/4 D256 20.4 -> 6.26.
     // Long contexts use 2-wave workgroups, two per CU (64 KB of LDS stages
     // each): measured ~5 % faster at 32K than one 4-wave workgroup per CU.
     const int blocks = (visible + kTok - 1) / kTok;
-    if (D > 128 || blocks <= kMW * 4) p.mw = kMW;
+    const bool whole = blocks <= kMW * 4 && units >= kMfmaTargetWG;  // one workgroup per unit
+    if (D > 128 || whole) p.mw = kMW;
     else p.mw = (int64_t)units * blocks <= 1024 ? 1 : 2;
     if (D <= 128 && (kEnvMw == 1 || kEnvMw == 2 || kEnvMw == kMW)) p.mw = kEnvMw;  // tuning override
     const int tile = p.mw * kTok;
@@ -1071,7 +1075,7 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     // (the waves past the split's keys contribute nothing).  Measured at
     // cfg4's 1024-key window: 32 splits per kv head 9.3 us, 8 splits 11.6 us.
     if (D > 128 && splits < want) splits = std::min(want, blocks);
-    if (blocks <= kMW * 4) splits = 1;
+    if (whole) splits = 1;
     const int cap = kMaxSplits;
     if (splits > cap) splits = cap;
     if (kEnvSplitsM >= 1) splits = kEnvSplitsM < cap ? kEnvSplitsM : cap;  // tuning override
@@ -1104,16 +1108,17 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
 // count is not monotonic in the length: short contexts use more, smaller
 // splits): every split holds at least one 32-key block (16 keys at
 // head_dim 256), at most kMaxSplits exist, and contexts of at most kMW * 4
-// blocks use one split.
+// blocks use one split when the units fill the chip.
 size_t decode_mfma_workspace(int batch, int n_head, int n_kv_head, int D, int max_len,
                              int window) {
     const MfmaPlan p = plan_mfma(batch, n_head, n_kv_head, D, max_len, window);
     const int visible = (window > 0 && max_len > window) ? window : max_len;
     const int blocks = (visible + kTok - 1) / kTok;
     // head_dim 256 may split down to 16-key blocks.
-    const int smax = blocks <= kMW * 4 ? 1 : std::min(kMaxSplits, D > 128 ? 2 * blocks : blocks);
-    if (smax <= 1) return 0;
     const size_t units = (size_t)batch * p.n_units;
+    const bool whole = blocks <= kMW * 4 && units >= (size_t)kMfmaTargetWG;
+    const int smax = whole ? 1 : std::min(kMaxSplits, D > 128 ? 2 * blocks : blocks);
+    if (smax <= 1) return 0;
     const size_t ml = (units * smax * p.gt * 2 * 4 + 255) / 256 * 256;
     return ml + units * smax * p.gt * D * 4;
 }
