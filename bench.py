@@ -685,7 +685,8 @@ def main():
                               "tflops": round(res["cfg3_paged"]["tflops"], 2)}},
         "cfg1_decode": {"workload": "cfg1 Llama-3.2-1B-shaped decode: 32/8 heads, head_dim 64, "
                                     "f32 KV 512, 28 layers per graph (rotated past the MALL)",
-                        "kernel": "decode_split_kernel (f32 VALU) + decode_merge_kernel",
+                        "kernel": "decode_block_kernel<F32,64,1,1> (bf16 hi + lo MFMA) + "
+                                  "decode_merge_kernel",
                         "us_per_layer": round(c1["us_per_layer"], 3),
                         "algorithmic_bytes": int(c1["layer_bytes"]),
                         "gbps": round(c1["gbps_step"], 1),

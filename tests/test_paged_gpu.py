@@ -95,8 +95,10 @@ def test_paged_vs_oracle(dev, case):
     ref = oracle_ref(q, kc, vc, lens, H, Hk, D, window, Hk * D + pad)
     for b in range(B):
         assert_close(o[b].reshape(-1), ref[b], what=f"case {case} b={b}")
-    if window == 0:
-        # same blocks and splits as the contiguous path: identical bits
+    if window == 0 and dt != "f32":
+        # same blocks and splits as the contiguous path: identical bits (an
+        # f32 cache's contiguous short splits run on the MFMA block kernel,
+        # its pages on decode_split_kernel: both checked against the oracle)
         ws = A.new_decode_workspace(B, H, Hk, D, L_, 0, dev)
         oc = A.attn_decode(q, kc, vc, sl, L_, Hk, kv_stride=Hk * D + pad, seq_stride=L_ * (Hk * D + pad),
                            workspace=ws)

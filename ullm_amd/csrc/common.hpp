@@ -109,12 +109,17 @@ inline bool dtype_ok(int dt) { return dt == ULLM_DT_F32 || dt == ULLM_DT_F16 || 
 // and (m, l) [units][splits][gt][2] f32, units = batch * n_units.
 void decode_merge_launch(int D, const float *ws_ml, const float *ws_acc, int splits, int gt,
                          int n_units, int batch, int n_head, float *out, hipStream_t st);
-// MFMA decode path for f16/bf16 caches (decode_mfma.hip).
+// MFMA decode path for f16/bf16 caches, and f32 caches on short splits
+// (decode_mfma.hip).
 size_t decode_mfma_plan_bytes(int batch, int n_head, int n_kv_head, int D, int max_len, int window);
 size_t decode_mfma_workspace(int batch, int n_head, int n_kv_head, int D, int max_len, int window);
 int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64_t kvs,
                 int64_t ss, const int32_t *lens, int max_len, int win, int batch, int nh, int nkv,
                 int D, float qs, float *out, void *ws, size_t ws_bytes, hipStream_t st);
+// Whether an f32-cache decode runs on the MFMA block kernel (decode_mfma
+// with ULLM_DT_F32), and that plan's workspace bytes.
+bool decode_f32_block_plan(int batch, int n_head, int n_kv_head, int D, int max_len, int window,
+                           size_t *bytes);
 
 // f32-cache split-KV decode over a paged cache (decode.hip).
 size_t decode_f32_workspace(int batch, int n_head, int n_kv_head, int D, int max_len, int window);

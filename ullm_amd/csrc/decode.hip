@@ -410,6 +410,13 @@ extern "C" int ullm_hip_attn_decode(const float *q, const void *k_cache, const v
         return decode_mfma(kv_dtype, q, k_cache, v_cache, kv_stride, seq_stride, seq_lens, max_len,
                            window, batch, n_head, n_kv_head, head_dim, qscale, out, workspace,
                            workspace_bytes, st);
+    // Short splits of an f32 cache run on the MFMA block kernel (bf16 hi + lo
+    // products); the rest on decode_split_kernel below.
+    size_t fb = 0;
+    if (decode_f32_block_plan(batch, n_head, n_kv_head, head_dim, max_len, window, &fb))
+        return decode_mfma(kv_dtype, q, k_cache, v_cache, kv_stride, seq_stride, seq_lens, max_len,
+                           window, batch, n_head, n_kv_head, head_dim, qscale, out, workspace,
+                           workspace_bytes, st);
     DecodePlan p = plan_decode(batch, n_head, n_kv_head, head_dim, kv_dtype, max_len, window);
     if (p.bytes > 0 && (!workspace || workspace_bytes < p.bytes))
         return set_error(ULLM_HIP_E_WORKSPACE, "decode: workspace of %zu bytes needed, %zu given",
@@ -512,10 +519,11 @@ extern "C" int ullm_hip_attn_decode_noalloc(const float *q, const void *k_cache,
     int rc = validate_decode(kv_dtype, kv_stride, max_len, batch, n_head, n_kv_head, head_dim);
     if (rc) return rc;
     // This call's partials (its own plan, not the bound over shorter calls).
-    const size_t need =
-        kv_dtype == ULLM_DT_F32
-            ? plan_decode(batch, n_head, n_kv_head, head_dim, kv_dtype, max_len, window).bytes
-            : decode_mfma_plan_bytes(batch, n_head, n_kv_head, head_dim, max_len, window);
+    size_t need = 0;
+    if (kv_dtype != ULLM_DT_F32)
+        need = decode_mfma_plan_bytes(batch, n_head, n_kv_head, head_dim, max_len, window);
+    else if (!decode_f32_block_plan(batch, n_head, n_kv_head, head_dim, max_len, window, &need))
+        need = plan_decode(batch, n_head, n_kv_head, head_dim, kv_dtype, max_len, window).bytes;
     if (need > kScratchBytes)
         return set_error(ULLM_HIP_E_WORKSPACE,
                          "decode_noalloc: this shape needs %zu bytes of split partials, above the "

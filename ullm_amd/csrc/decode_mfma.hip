@@ -28,6 +28,7 @@
 //    LDS; the splits of a unit are combined by decode_merge_kernel.
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 #include "common.hpp"
 #include "mfma_util.hpp"
 #include "wave.hpp"
@@ -710,14 +711,20 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
     constexpr int NS = D / 32;          // QK k-steps (32 d each)
     constexpr int NDT = D / 16;         // 16-wide d tiles of O^T
     constexpr int NDW = NDT / CW;       // d tiles per wave
-    constexpr int RB = D * 2;           // bytes per key row of one head
-    constexpr int SLOTS = D / 8;        // 16-byte slots per row
+    // An f32 cache (the reference's) runs both contractions on bf16 MFMAs
+    // over hi + lo halves: Q.K = Khi.Qhi + Khi.Qlo + Klo.Qhi and
+    // P.V = Vhi.Phi + Vhi.Plo + Vlo.Phi (about 2^-16 of each product).
+    constexpr bool F = __is_same(T, F32);
+    using MT = typename std::conditional<F, BF16, T>::type;  // MFMA operand type
+    constexpr int RB = D * T::bytes;    // bytes per key row of one head
+    constexpr int SLOTS = RB / 16;      // 16-byte slots per row
     constexpr int RPI = 1024 / RB;      // rows written by one DMA instruction
     constexpr int NI = KB / RPI;        // DMA instructions per K (or V) tile
     constexpr int NIW = NI / CW;        // ... per wave
     constexpr int TILE = KB * RB;
     constexpr int NT = KB / 16;         // 16-key tiles per block
-    constexpr bool SPLITP = __is_same(T, BF16);
+    constexpr bool SPLITP = !__is_same(T, F16);
+    static_assert(!F || (CW == 1 && KB == 32), "f32: one wave, 32-key blocks");
     static_assert(D == 64 || D == 128 || D == 256, "head_dim 64, 128, 256");
     static_assert(KB == 16 || KB == 32, "keys per block");
     static_assert(NIW >= 1 && NDW >= 1, "quarter tiles");
@@ -745,10 +752,11 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
     const int c0 = (fetch_len > 0 ? 0 : start) + split * chunk;
     const int cf = fetch_len > 0 ? min(c0 + chunk, fetch_len) : min(c0 + chunk, len);
 
-    const int rb = (int)(kv_stride * 2);
-    const char *kb0 = kc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
-    const char *vb0 = vc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
-    const int range = cf > 0 ? (cf - 1) * rb + D * 2 : 0;
+    constexpr int EB = T::bytes;  // cache element bytes
+    const int rb = (int)(kv_stride * EB);
+    const char *kb0 = kc + (int64_t)b * seq_stride * EB + (int64_t)kvh * RB;
+    const char *vb0 = vc + (int64_t)b * seq_stride * EB + (int64_t)kvh * RB;
+    const int range = cf > 0 ? (cf - 1) * rb + RB : 0;
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kb0), 0, range, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t vrs =
@@ -797,7 +805,7 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
         for (int j = 0; j < 4; j++) {
             const float x0 = head_ok ? qa[s][j >> 1][(2 * j) & 3] * qscale : 0.f;
             const float x1 = head_ok ? qa[s][j >> 1][(2 * j + 1) & 3] * qscale : 0.f;
-            const u32x2 hl = split2<T>(x0, x1);
+            const u32x2 hl = split2<MT>(x0, x1);
             qh[s][j] = hl[0];
             ql[s][j] = hl[1];
         }
@@ -822,13 +830,18 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             return;
         }
         const uint32_t kbase = lds_addr(lds + 2 * bi * TILE);
-        u32x4 ka[NT * NS];
+        // lane (key t*16 + n16, k-group kg): d = s*32 + kg*8 .. +7
+        constexpr int KR = F ? 2 : 1;  // 16-byte reads per operand
+        u32x4 ka[NT * NS * KR];
 #pragma unroll
         for (int t = 0; t < NT; t++) {
             const int r = t * 16 + n16;
 #pragma unroll
             for (int s = 0; s < NS; s++)
-                ka[t * NS + s] = lds_read_b128(kbase + r * RB + (((s * 4 + kg) ^ (r & (SLOTS - 1))) * 16));
+#pragma unroll
+                for (int h = 0; h < KR; h++)
+                    ka[(t * NS + s) * KR + h] =
+                        lds_read_b128(kbase + r * RB + ((((s * 4 + kg) * KR + h) ^ (r & (SLOTS - 1))) * 16));
         }
         lds_wait(ka);
         f32x4 sacc[2];
@@ -838,8 +851,24 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < NS; s++) {
-                sacc[t] = mfma16<T>(ka[t * NS + s], qh[s], sacc[t]);
-                sacc[t] = mfma16<T>(ka[t * NS + s], ql[s], sacc[t]);
+                if constexpr (F) {
+                    const u32x4 a = ka[(t * NS + s) * 2], c = ka[(t * NS + s) * 2 + 1];
+                    u32x4 kh, kl;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const u32x4 &src = j < 2 ? a : c;
+                        const u32x2 hl = split2<BF16>(__uint_as_float(src[(2 * j) & 3]),
+                                                      __uint_as_float(src[(2 * j + 1) & 3]));
+                        kh[j] = hl[0];
+                        kl[j] = hl[1];
+                    }
+                    sacc[t] = mfma16<BF16>(kh, qh[s], sacc[t]);
+                    sacc[t] = mfma16<BF16>(kh, ql[s], sacc[t]);
+                    sacc[t] = mfma16<BF16>(kl, qh[s], sacc[t]);
+                } else {
+                    sacc[t] = mfma16<T>(ka[t * NS + s], qh[s], sacc[t]);
+                    sacc[t] = mfma16<T>(ka[t * NS + s], ql[s], sacc[t]);
+                }
             }
         }
         float sv[8];
@@ -873,7 +902,7 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             if constexpr (SPLITP) {
-                const u32x2 hl = split2<T>(p[2 * j], p[2 * j + 1]);
+                const u32x2 hl = split2<MT>(p[2 * j], p[2 * j + 1]);
                 ph[j] = hl[0];
                 pl[j] = hl[1];
             } else {
@@ -894,6 +923,38 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
         }
         const int vr0 = kg * 4 + (n16 >> 2);
         u32x4 va[NDW];
+        if constexpr (F) {
+            // V^T operand gathered from the f32 rows: lane (d = dt*16 + n16,
+            // kg) takes rows kg*4 + j and 16 + kg*4 + j (j < 4) of column d,
+            // then splits them into bf16 hi (va) and lo (vl) halves.
+            u32x4 vl[NDW];
+            float vv[NDW][8];
+#pragma unroll
+            for (int i = 0; i < NDW; i++) {
+                const int d = i * 16 + n16;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int r = (j >> 2) * 16 + kg * 4 + (j & 3);
+                    vv[i][j] = *(const float *)(lds + (2 * bi + 1) * TILE + r * RB +
+                                                (((d >> 2) ^ (r & (SLOTS - 1))) * 16) + (d & 3) * 4);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NDW; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const u32x2 hl = split2<BF16>(vv[i][2 * j], vv[i][2 * j + 1]);
+                    va[i][j] = hl[0];
+                    vl[i][j] = hl[1];
+                }
+#pragma unroll
+            for (int i = 0; i < NDW; i++) {
+                oacc[i] = mfma16<BF16>(va[i], ph, oacc[i]);
+                oacc[i] = mfma16<BF16>(va[i], pl, oacc[i]);
+                oacc[i] = mfma16<BF16>(vl[i], ph, oacc[i]);
+            }
+            return;
+        } else {
 #pragma unroll
         for (int i = 0; i < NDW; i++) {
             const int dt = wave * NDW + i;
@@ -914,6 +975,7 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             oacc[i] = mfma16<T>(va[i], ph, oacc[i]);
             if constexpr (SPLITP) oacc[i] = mfma16<T>(va[i], pl, oacc[i]);
         }
+        }
     });
     __builtin_amdgcn_s_waitcnt(vm_wait(0));  // no DMA may outlive the workgroup
     l_part = rows_sum(l_part);
@@ -932,6 +994,9 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             *(float2 *)(ws_ml + ((u * splits + split) * gt + n16) * 2) = float2{m_run, l_part};
     }
 }
+
+// CW > 1 instances of decode_block_kernel exist for f16/bf16 caches only.
+template <class T> using MaybeF16 = typename std::conditional<__is_same(T, F32), F16, T>::type;
 
 constexpr int kMaxSplits = 256;
 
@@ -1218,24 +1283,39 @@ static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const
                                (float *)(ws + p.off_acc));
             };
             if (p.chunk == 2 * kTok) go(decode_block_kernel<T, D, 1, 2>, 1);
-            else if (kEnvCw == 2) go(decode_block_kernel<T, D, 2, 1>, 2);
-            else if (kEnvCw == 4) go(decode_block_kernel<T, D, 4, 1>, 4);
+            else if (!__is_same(T, F32) && kEnvCw == 2) go(decode_block_kernel<MaybeF16<T>, D, 2, 1>, 2);
+            else if (!__is_same(T, F32) && kEnvCw == 4) go(decode_block_kernel<MaybeF16<T>, D, 4, 1>, 4);
             else go(decode_block_kernel<T, D, 1, 1>, 1);
             launch_merge<D>(p, batch, nh, out, ws, st);
             return;
         }
     }
+    if constexpr (__is_same(T, F32)) return;  // f32 comes here only for block plans
+    else {
     MainLaunch<T, D>::run(p.mw, dim3(p.splits, p.n_units, batch), st, q, (const char *)kc,
                           (const char *)vc, kvs, ss, lens, win, fetch_len, nh, kv_mul, p.gt,
                           p.n_units,
                           p.chunk, p.splits, qs, out, (float *)(ws + p.off_ml),
                           (float *)(ws + p.off_acc));
     if (p.splits > 1) launch_merge<D>(p, batch, nh, out, ws, st);
+    }
 }
 
 size_t decode_mfma_plan_bytes(int batch, int n_head, int n_kv_head, int D, int max_len,
                               int window) {
     return plan_mfma(batch, n_head, n_kv_head, D, max_len, window).bytes;
+}
+
+// The reference's f32 cache on decode_block_kernel, where the f16/bf16 plan
+// cuts one- or two-block splits (head_dim 64/128, contiguous cache); *bytes
+// is that plan's workspace.  Other f32 requests stay on decode_split_kernel.
+bool decode_f32_block_plan(int batch, int n_head, int n_kv_head, int D, int max_len, int window,
+                           size_t *bytes) {
+    if (D > 128 || kNoBlock) return false;
+    const MfmaPlan p = plan_mfma(batch, n_head, n_kv_head, D, max_len, window);
+    if (!(p.mw == 1 && (p.chunk == kTok || p.chunk == 2 * kTok) && p.splits > 1)) return false;
+    *bytes = p.bytes;
+    return true;
 }
 
 int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64_t kvs,
@@ -1251,7 +1331,10 @@ int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64
 #define ULLM_MFMA_CASE(TT, DD) \
     launch_mfma<TT, DD>(p, q, kc, vc, kvs, ss, lens, max_len, win, batch, nh, kv_mul, qs, \
                         out, w, st)
-    if (dtype == ULLM_DT_F16) {
+    if (dtype == ULLM_DT_F32) {
+        if (D == 64) ULLM_MFMA_CASE(F32, 64);
+        else ULLM_MFMA_CASE(F32, 128);
+    } else if (dtype == ULLM_DT_F16) {
         if (D == 64) ULLM_MFMA_CASE(F16, 64);
         else if (D == 128) ULLM_MFMA_CASE(F16, 128);
         else ULLM_MFMA_CASE(F16, 256);
