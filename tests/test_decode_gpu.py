@@ -73,7 +73,7 @@ def test_cfg4_gemma3_f16_8k(dev, window):
 
 
 # Splits of one or two 32-key blocks, or of one 16-key block at head_dim 256
-# (decode_block_kernel): a last split that
+# (decode_block_kernel; f16, bf16 and the f32 cache): a last split that
 # fetches only the first of its two blocks (8152), one whose second block
 # ends inside the length (8100), binding windows that start off a block
 # boundary, head_dim 64.
@@ -83,7 +83,10 @@ def test_cfg4_gemma3_f16_8k(dev, window):
     ("f16", 32, 8, 64, 2047, 0), ("bf16", 16, 2, 128, 4000, 3000),
     # head_dim 256 on 16-key splits: a binding window ending mid-block, and
     # a fetched range ending mid-block
-    ("bf16", 8, 4, 256, 3000, 1000), ("f16", 16, 8, 256, 700, 0)])
+    ("bf16", 8, 4, 256, 3000, 1000), ("f16", 16, 8, 256, 700, 0),
+    # the reference's f32 cache on the block kernel (bf16 hi + lo products)
+    ("f32", 12, 2, 128, 8152, 0), ("f32", 12, 2, 128, 8100, 0), ("f32", 8, 4, 64, 2000, 1500),
+    ("f32", 32, 8, 64, 2047, 0), ("f32", 16, 2, 128, 4000, 3000), ("f32", 32, 8, 64, 100, 0)])
 def test_block_splits(dev, dtype, H, Hk, D, L, window):
     run_case(dev, dtype, H, Hk, D, [L], window=window, seed=13)
 
