@@ -1133,7 +1133,14 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     if (D <= 128 && (kEnvMw == 1 || kEnvMw == 2 || kEnvMw == kMW)) p.mw = kEnvMw;  // tuning override
     const int tile = p.mw * kTok;
     int splits = (visible + tile - 1) / tile;
-    const int want = (kMfmaTargetWG * (p.mw == kMW ? 1 : 2) + units - 1) / units;
+    int want = (kMfmaTargetWG * (p.mw == kMW ? 1 : 2) + units - 1) / units;
+    // Long-context batches: chunks of at most 22 blocks.  The sequences'
+    // lengths are on the device, and a ragged batch leaves the splits past
+    // each short sequence idle, so the busy ones must be small enough to
+    // spread evenly.  cfg5 batch 8 ragged (us/layer): 16 splits 63.6, 32
+    // 61.2, 44 56.0, 48 55.0, 52 58.0, 96 60.0; uniform batches lose 3-4 %
+    // (8 x 16K keys: 49.4 at 16 splits, 51.3 at 48).
+    if (batch > 1 && p.mw == 2) want = std::max(want, (visible + 22 * kTok - 1) / (22 * kTok));
     if (splits > want) splits = want;
     // head_dim 256 (4-wave workgroups): a short context would leave most CUs
     // idle at one tile per split, so splits go down to one 32-key block
@@ -1264,7 +1271,9 @@ static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const
                         hipStream_t st) {
     // Keys 0..max_len-1 of every sequence are readable (the cache holds them);
     // when the window cannot bind, the kernels fetch keys before the length.
-    const int fetch_len = (win <= 0 || max_len <= win) ? max_len : 0;
+    // Only for one sequence (whose length is normally max_len): in a ragged
+    // batch the splits past a short sequence's length would fetch for nothing.
+    const int fetch_len = batch == 1 && (win <= 0 || max_len <= win) ? max_len : 0;
     if constexpr (D > 128) {
         if (p.kb == 16) {
             hipLaunchKernelGGL((decode_block_kernel<T, D, 1, 1, 16>), dim3(p.splits, p.n_units, batch),
