@@ -224,5 +224,8 @@ __device__ __forceinline__ void page_tile(const KvPages &pg, const char *kc, con
 int launch_prefill16(int dtype, const void *q, const void *kc, const void *vc, int64_t kvs, int S,
                      int start_pos, int window, int n_head, int kv_mul, float qs, float *out,
                      hipStream_t st, KvPages pgs);
+int launch_prefill16_128(int dtype, const void *q, const void *kc, const void *vc, int64_t kvs,
+                         int S, int start_pos, int window, int n_head, int kv_mul, float qs,
+                         float *out, hipStream_t st, KvPages pgs);
 
 }  // namespace ullm

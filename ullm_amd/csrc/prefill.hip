@@ -11,6 +11,8 @@
 // online softmax in the exp2 domain (scale*log2(e) folded into one multiply),
 // QK^T on v_mfma_f32_32x32x16_{bf16,f16} and P.V on the f16 variant (P and a
 // bf16 V rounded to f16: 2^-11 relative, where bf16 P would cost 2^-8):
+//  * prefill16_kernel (prefill16.hip) for head_dim 256, and for head_dim 128
+//    when a prompt is too short for prefill4_kernel's pairs to fill the chip;
 //  * prefill4_kernel (head_dim <= 128, no binding window): 8-wave
 //    workgroups over a pair of causal row blocks, split-K between two
 //    4-wave sets, K/V tiles shared through an LDS ring filled by DMA;
@@ -1166,6 +1168,19 @@ void PrefillLaunch<T, D, true>::run(const void *q, const void *kc, const void *v
     const int paired = !(win > 0 && win < sp + S);
     const int total = n_units * np;
     const int per_xcd = (total + 7) / 8;
+    // head_dim 128, short prompts: prefill16_kernel (16-row waves; K/V tiles
+    // shared by the GQA group; two key streams when units are few) when
+    // prefill4's causal pairs would cover half the CUs or fewer.  Measured
+    // (us, prefill4 -> prefill16): 12/2 heads S=1024 26.2 -> 16.5, S=2048
+    // 39.4 -> 29.6; 32/8 heads S=512 18.8 -> 12.0, S=1024 27.3 -> 23.7,
+    // S=1536 (192 pairs) 39.7 -> 42.6, S=2048 (256) 51.8 -> 59.9.
+    // ULLM_HIP_PREFILL128=16 / =4 forces either kernel (tuning override).
+    static const int e128 = env_override("ULLM_HIP_PREFILL128");
+    if (D == 128 && (e128 == 16 || (e128 != 4 && paired && total <= 128))) {
+        launch_prefill16_128(__is_same(T, BF16) ? ULLM_DT_BF16 : ULLM_DT_F16, q, kc, vc, kvs, S, sp,
+                             win, nh, kv_mul, qs, out, st, pgs);
+        return;
+    }
     if (D <= 128 && paired) {
         const int lhw = hw == 4 ? 2 : (hw == 2 ? 1 : 0);
         hipLaunchKernelGGL((prefill4_kernel<T, D>), dim3(per_xcd * 8), dim3(512), 0, st,

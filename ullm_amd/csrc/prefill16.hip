@@ -1,4 +1,6 @@
-// Causal prefill at head_dim 256 with 16-row waves, two per SIMD (gfx950).
+// Causal prefill with 16-row waves, two per SIMD (gfx950): head_dim 256, and
+// head_dim 128 for short prompts (prefill.hip picks it where prefill4_kernel's
+// causal pairs would leave half the CUs idle).
 //
 // Computes, for query row s (pos = start_pos + s) of head h,
 // out = softmax_t(scale q.K[t]) . V[t] over t in the window start .. pos: the
@@ -18,7 +20,7 @@
 //    from ds_read_b64_tr_b16 on the row-major V tile, reading rows 4g..4g+3
 //    and 16+4g..16+4g+3 so the key orders match.
 //  * O for 16 rows x 256 d is 64 registers (128 at 32 rows), so a wave needs
-//    ~214 registers and two waves share each SIMD: one wave's softmax VALU
+//    ~214 registers (~130 at head_dim 128) and two waves share each SIMD: one wave's softmax VALU
 //    work and LDS waits overlap the other's MFMAs, which a lone wave per
 //    SIMD (the 32-row layout at D = 256) cannot arrange for itself.
 //
@@ -61,22 +63,25 @@ namespace ullm {
 __device__ __forceinline__ int p16_kswz(int r) { return r & 15; }
 __device__ __forceinline__ int p16_vswz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
-// Ring stages per key stream: as many K/V stages as 160 KB holds, at most 4.
-template <int KS, int DS>
+// Ring stages per key stream: as many K/V stages as a workgroup's share of
+// 160 KB holds (OCC workgroups per CU), at most 4.
+template <int KS, int DS, int D, int OCC>
 constexpr int p16_stages() {
-    constexpr int st = 160 * 1024 / (KS * (32 * 512 + 32 * 512 / DS));
+    constexpr int st = 160 * 1024 / OCC / (KS * (32 * D * 2 + 32 * D * 2 / DS));
     return st > 4 ? 4 : st;
 }
 
-template <class T, int KS, int DS, int NSTG = p16_stages<KS, DS>()>
-__global__ __launch_bounds__(512, 1) void prefill16_kernel(
+template <class T, int KS, int DS, int D = 256, int OCC = 1,
+          int NSTG = p16_stages<KS, DS, D, OCC>()>
+__global__ __launch_bounds__(512, OCC) void prefill16_kernel(
     const uint16_t *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int S, int start_pos, int window, int n_head, int kv_mul, int hw,
     int n_hg, int n_units, float qscale, float *__restrict__ out, KvPages pgs) {
     // DS = 2: the workgroup computes the full Q.K and softmax of its rows but
     // P.V and the output for one half of the 256 value columns only; its V
     // tiles hold that half (256-byte rows).
-    constexpr int D = 256, BN = 32, RB = D * 2, RBV = RB / DS;
+    constexpr int BN = 32, RB = D * 2, RBV = RB / DS;
+    static_assert(D == 128 || D == 256, "head_dim");
     constexpr int TILE = BN * RB, TILEV = BN * RBV, STAGE = TILE + TILEV;
     constexpr int NW = 8, NWS = NW / KS;  // waves per stream
     constexpr int NIC = TILE / 1024 / NWS;    // 1 KiB DMA chunks per wave, K
@@ -86,7 +91,11 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
     constexpr float kLazy = 8.0f;
     static_assert(KS == 1 || KS == 2, "key streams");
     static_assert(DS == 1 || DS == 2, "value column split");
-    static_assert(NSTG >= 2 && KS * NSTG * STAGE <= 160 * 1024, "LDS ring");
+    static_assert(NSTG >= 2 && KS * NSTG * STAGE <= 160 * 1024 / OCC, "LDS ring");
+    static_assert(NIC >= 1 && NICV >= 1, "DMA chunks per wave");
+    // The V swizzle permutes the 16 slots of each 256-byte half of a row: V
+    // rows of at least 256 bytes (no value split at head_dim 128).
+    static_assert(RBV >= 256, "V rows of 256 bytes or more");
     __shared__ __attribute__((aligned(1024))) char lds[KS * NSTG * STAGE];
 
     const int dh = DS == 1 ? 0 : (int)(blockIdx.x % DS);  // value half
@@ -130,8 +139,9 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
     int kofs[NIC], vofs[NICV];
 #pragma unroll
     for (int i = 0; i < NIC; i++) {
-        const int r = (ws * NIC + i) * 2 + (lane >> 5);
-        kofs[i] = r * rbg + (((lane & 31) ^ p16_kswz(r)) * 16);
+        constexpr int KSL = RB / 16;  // 16-byte slots per K row
+        const int r = (ws * NIC + i) * (1024 / RB) + lane / KSL;
+        kofs[i] = r * rbg + (((lane % KSL) ^ p16_kswz(r)) * 16);
     }
     // A V chunk is 1024 / RBV rows; slot c of row r takes the row's value
     // chunk (c ^ p16_vswz(r)) of half dh.
@@ -139,7 +149,7 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
 #pragma unroll
     for (int i = 0; i < NICV; i++) {
         const int r = (ws * NICV + i) * (1024 / RBV) + lane / VSL;
-        vofs[i] = r * rbg + ((((lane % VSL) ^ p16_vswz(r)) + dh * 16) * 16);
+        vofs[i] = r * rbg + ((((lane % VSL) ^ p16_vswz(r)) + dh * VSL) * 16);
     }
     char *const ring = lds + ks * NSTG * STAGE;
     auto issue = [&](int j) {  // step j's tile of this stream into stage j % NSTG
@@ -220,8 +230,8 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
         for (int i = 0; i < 4; i++) kaddr[i] = sb + ka[i];
 #pragma unroll
         for (int i = 0; i < 8; i++) vaddr[i] = sb + va[i];
-        u32x4 kb[16];
-        static_for<0, 16>([&](auto ic) {
+        u32x4 kb[2 * NKS];
+        static_for<0, 2 * NKS>([&](auto ic) {
             constexpr int idx = decltype(ic)::value, s = idx >> 1, kt = idx & 1;
             kb[idx] = lds_read_b128_at<(s >> 2) * 256 + kt * 16 * RB>(kaddr[s & 3]);
         });
@@ -232,14 +242,14 @@ __global__ __launch_bounds__(512, 1) void prefill16_kernel(
             const u32x2 hi = lds_read_tr16_b64_at<(dt >> 3) * 256 + 16 * RBV>(vaddr[dt & 7]);
             vb[dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         };
-        asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
-        static_for<0, 16>([&](auto ic) {
+        lds_wait_n<NKS>();  // the first half of the K reads
+        static_for<0, 2 * NKS>([&](auto ic) {
             constexpr int idx = decltype(ic)::value, s = idx >> 1, kt = idx & 1;
-            if constexpr (idx == 8) asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+            if constexpr (idx == NKS) asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
             tie(kb[idx]);
             sacc[kt] = mfma16<T>(kb[idx], qreg[s], sacc[kt]);
             if constexpr (idx == 0) { rdv(Int<0>{}); rdv(Int<1>{}); rdv(Int<2>{}); rdv(Int<3>{}); }
-            if constexpr (idx == 8) { rdv(Int<4>{}); rdv(Int<5>{}); rdv(Int<6>{}); rdv(Int<7>{}); }
+            if constexpr (idx == NKS) { rdv(Int<4>{}); rdv(Int<5>{}); rdv(Int<6>{}); rdv(Int<7>{}); }
         });
         // Mask where the tile reaches past the wave's first row or before the
         // window of its last (wave-uniform test): key - pos_row must lie in
@@ -425,6 +435,30 @@ int launch_prefill16(int dtype, const void *q, const void *kc, const void *vc, i
     if (dtype == ULLM_DT_BF16) pick(BF16{});
     else pick(F16{});
     return check_hip(hipGetLastError(), "prefill (16-row waves) launch");
+}
+
+// head_dim 128 on prefill16_kernel (short prompts; no value split).
+int launch_prefill16_128(int dtype, const void *q, const void *kc, const void *vc, int64_t kvs,
+                         int S, int start_pos, int window, int n_head, int kv_mul, float qs,
+                         float *out, hipStream_t st, KvPages pgs) {
+    int KS, DS;  // head_dim 128: no value split (V rows of 256 bytes)
+    prefill16_plan(S, start_pos, window, n_head, kv_mul, KS, DS);
+    const int hw = p16_hw(kv_mul, 8 / KS), UR = 16 * (8 / KS) / hw;
+    const int n_units = (S + UR - 1) / UR, n_hg = n_head / hw;
+    const dim3 grid((unsigned)(n_units * n_hg));
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(512), 0, st, (const uint16_t *)q, (const char *)kc,
+                           (const char *)vc, kvs, S, start_pos, window, n_head, kv_mul, hw, n_hg,
+                           n_units, qs, out, pgs);
+    };
+    auto pick = [&](auto t) {
+        using T = decltype(t);
+        if (KS == 2) go(prefill16_kernel<T, 2, 1, 128, 1>);
+        else go(prefill16_kernel<T, 1, 1, 128, 1>);
+    };
+    if (dtype == ULLM_DT_BF16) pick(BF16{});
+    else pick(F16{});
+    return check_hip(hipGetLastError(), "prefill (16-row waves, head_dim 128) launch");
 }
 
 }  // namespace ullm
