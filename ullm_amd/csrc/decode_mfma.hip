@@ -689,28 +689,25 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
                        out, ws_ml, ws_acc);
 }
 
-// Splits of one 32-key block (short contexts: cfg2 cuts 4096 keys into 128
-// splits per kv head).  Straight-line code for the one block: q loads, the
-// block's K and V DMA, S^T = K.Q^T and the softmax once K has landed, then
-// O^T += V^T.P^T and the split's store.  CW waves may share the block: each
-// fetches 1/CW of the K and V tiles and, after a barrier, computes the full
-// Q.K and softmax (the same values in each) and P.V for its 1/CW of the d
-// tiles.  Measured at cfg2 (us per layer, graph of 28 layers): CW 1 6.44,
-// 2 6.45, 4 6.65, 8 7.31, against 6.92 for the same splits on
-// decode_dma_kernel's one-wave workgroups (its two-stage loop around the
-// one block).  Same arguments, masks and partial layout as
-// decode_dma_kernel (chunk = NB * KB).  KB = 16 (head_dim 256): a block is one
-// 16-key tile, so a short context spreads over twice the workgroups; the
-// P^T operand's keys 16-31 are zero.
-template <class T, int D, int CW, int NB, int KB = kTok>
-__global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
+// Splits of one or two blocks (short contexts: cfg2 cuts 4096 keys into 128
+// one-block splits per kv head), on one-wave workgroups.  Straight-line code:
+// q loads, the DMA of every block's K and V tiles at once, then per block
+// S^T = K.Q^T and the softmax once its K has landed, O^T += V^T.P^T once its
+// V has, and the split's store.  Measured at cfg2: 6.44 us per layer (graph
+// of 28 layers) against 6.92 for the same splits on decode_dma_kernel's
+// one-wave workgroups (its two-stage loop around the one block); sharing the
+// block among 2, 4 or 8 waves measured 6.45, 6.65 and 7.31.  Same arguments,
+// masks and partial layout as decode_dma_kernel (chunk = NB * KB).  KB = 16
+// (head_dim 256): a block is one 16-key tile, so a short context spreads
+// over twice the workgroups; the P^T operand's keys 16-31 are zero.
+template <class T, int D, int NB, int KB = kTok>
+__global__ __launch_bounds__(64, 1) void decode_block_kernel(
     const float *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int64_t seq_stride, const int32_t *__restrict__ seq_lens, int window,
     int fetch_len, int n_head, int kv_mul, int gt, int n_units, int chunk, int splits, float qscale,
     float *__restrict__ out, float *__restrict__ ws_ml, float *__restrict__ ws_acc) {
     constexpr int NS = D / 32;          // QK k-steps (32 d each)
     constexpr int NDT = D / 16;         // 16-wide d tiles of O^T
-    constexpr int NDW = NDT / CW;       // d tiles per wave
     // An f32 cache (the reference's) runs both contractions on bf16 MFMAs
     // over hi + lo halves: Q.K = Khi.Qhi + Khi.Qlo + Klo.Qhi and
     // P.V = Vhi.Phi + Vhi.Plo + Vlo.Phi (about 2^-16 of each product).
@@ -720,18 +717,15 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
     constexpr int SLOTS = RB / 16;      // 16-byte slots per row
     constexpr int RPI = 1024 / RB;      // rows written by one DMA instruction
     constexpr int NI = KB / RPI;        // DMA instructions per K (or V) tile
-    constexpr int NIW = NI / CW;        // ... per wave
     constexpr int TILE = KB * RB;
     constexpr int NT = KB / 16;         // 16-key tiles per block
     constexpr bool SPLITP = !__is_same(T, F16);
-    static_assert(!F || (CW == 1 && KB == 32), "f32: one wave, 32-key blocks");
+    static_assert(!F || KB == 32, "f32: 32-key blocks");
     static_assert(D == 64 || D == 128 || D == 256, "head_dim 64, 128, 256");
     static_assert(KB == 16 || KB == 32, "keys per block");
-    static_assert(NIW >= 1 && NDW >= 1, "quarter tiles");
 
     const int split = blockIdx.x, unit = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n16 = lane & 15, kg = lane >> 4;
     const int head0 = unit * gt, kvh = head0 / kv_mul;
     const bool head_ok = n16 < gt;
@@ -762,7 +756,7 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
     const __amdgpu_buffer_rsrc_t vrs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vb0), 0, range, kRsrcWord3);
 
-    // q first, then this wave's DMA instructions of every block: K0, V0, K1, ...
+    // q first, then the DMA instructions of every block: K0, V0, K1, ...
     // (a block wholly past the fetched range is not requested).
     f32x4 qa[NS][2];
     {
@@ -781,15 +775,15 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             if (bi < nfb) {
                 const int so = __builtin_amdgcn_readfirstlane((c0 + bi * KB) * rb);
 #pragma unroll
-                for (int i = 0; i < NIW; i++) {
-                    const int r = (wave * NIW + i) * RPI + drow;
-                    dma16(krs, lds + 2 * bi * TILE + (wave * NIW + i) * 1024,
+                for (int i = 0; i < NI; i++) {
+                    const int r = (i) * RPI + drow;
+                    dma16(krs, lds + 2 * bi * TILE + (i) * 1024,
                           r * rb + ((dslot ^ (r & (SLOTS - 1))) * 16) + so, 0);
                 }
 #pragma unroll
-                for (int i = 0; i < NIW; i++) {
-                    const int r = (wave * NIW + i) * RPI + drow;
-                    dma16(vrs, lds + (2 * bi + 1) * TILE + (wave * NIW + i) * 1024,
+                for (int i = 0; i < NI; i++) {
+                    const int r = (i) * RPI + drow;
+                    dma16(vrs, lds + (2 * bi + 1) * TILE + (i) * 1024,
                           r * rb + ((dslot ^ (r & (SLOTS - 1))) * 16) + so, 0);
                 }
             }
@@ -810,9 +804,9 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             ql[s][j] = hl[1];
         }
 
-    f32x4 oacc[NDW];
+    f32x4 oacc[NDT];
 #pragma unroll
-    for (int i = 0; i < NDW; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < NDT; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_part = 0.f;
     // Block bi: its K is waited for with V bi and the later blocks still
     // counted; its V with the later blocks counted.  Those counts hold when
@@ -822,9 +816,8 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
         constexpr int bi = decltype(bc)::value;
         const int tb = c0 + bi * KB;
         if (bi >= nfb) return;
-        if (nfb == NB) __builtin_amdgcn_s_waitcnt(vm_wait((2 * (NB - bi) - 1) * NIW));
+        if (nfb == NB) __builtin_amdgcn_s_waitcnt(vm_wait((2 * (NB - bi) - 1) * NI));
         else __builtin_amdgcn_s_waitcnt(vm_wait(0));
-        if constexpr (CW > 1) __syncthreads();
         if (tb >= c1) {  // fetched but past the length: nothing to add
             __builtin_amdgcn_s_waitcnt(vm_wait(0));
             return;
@@ -892,7 +885,7 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             const float corr = __builtin_amdgcn_exp2f(m_run - mu);
             l_part *= corr;
 #pragma unroll
-            for (int i = 0; i < NDW; i++) oacc[i] *= corr;
+            for (int i = 0; i < NDT; i++) oacc[i] *= corr;
         }
         m_run = m_new;
         float p[8];
@@ -909,28 +902,26 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
                 ph[j] = pack2<T>(p[2 * j], p[2 * j + 1]);
             }
         }
-        if (nfb == NB) __builtin_amdgcn_s_waitcnt(vm_wait(2 * (NB - bi - 1) * NIW));
+        if (nfb == NB) __builtin_amdgcn_s_waitcnt(vm_wait(2 * (NB - bi - 1) * NI));
         else __builtin_amdgcn_s_waitcnt(vm_wait(0));
-        if constexpr (CW > 1) __syncthreads();
         const uint32_t vbase = lds_addr(lds + (2 * bi + 1) * TILE);
         if (tb + KB > c1) {
             // Fetched rows at or past the length hold whatever the cache
-            // holds there (P is 0 for them, but 0 * NaN is NaN): each
-            // wave zeroes them before its own reads (the same zeros).
+            // holds there (P is 0 for them, but 0 * NaN is NaN): zero them.
             const int nv = max(c1 - tb, 0);
             for (int i = nv * SLOTS + lane; i < KB * SLOTS; i += 64)
                 lds_write_b128(vbase + i * 16, u32x4{0u, 0u, 0u, 0u});
         }
         const int vr0 = kg * 4 + (n16 >> 2);
-        u32x4 va[NDW];
+        u32x4 va[NDT];
         if constexpr (F) {
             // V^T operand gathered from the f32 rows: lane (d = dt*16 + n16,
             // kg) takes rows kg*4 + j and 16 + kg*4 + j (j < 4) of column d,
             // then splits them into bf16 hi (va) and lo (vl) halves.
-            u32x4 vl[NDW];
-            float vv[NDW][8];
+            u32x4 vl[NDT];
+            float vv[NDT][8];
 #pragma unroll
-            for (int i = 0; i < NDW; i++) {
+            for (int i = 0; i < NDT; i++) {
                 const int d = i * 16 + n16;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
@@ -940,7 +931,7 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
                 }
             }
 #pragma unroll
-            for (int i = 0; i < NDW; i++)
+            for (int i = 0; i < NDT; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const u32x2 hl = split2<BF16>(vv[i][2 * j], vv[i][2 * j + 1]);
@@ -948,7 +939,7 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
                     vl[i][j] = hl[1];
                 }
 #pragma unroll
-            for (int i = 0; i < NDW; i++) {
+            for (int i = 0; i < NDT; i++) {
                 oacc[i] = mfma16<BF16>(va[i], ph, oacc[i]);
                 oacc[i] = mfma16<BF16>(va[i], pl, oacc[i]);
                 oacc[i] = mfma16<BF16>(vl[i], ph, oacc[i]);
@@ -956,8 +947,8 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
             return;
         } else {
 #pragma unroll
-        for (int i = 0; i < NDW; i++) {
-            const int dt = wave * NDW + i;
+        for (int i = 0; i < NDT; i++) {
+            const int dt = i;
             const int ch = dt * 2 + ((n16 & 3) >> 1);
             const int bo = 8 * (n16 & 1);
             const u32x2 l2 = lds_read_tr16_b64(vbase + vr0 * RB + ((ch ^ (vr0 & (SLOTS - 1))) * 16) + bo);
@@ -971,7 +962,7 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
         }
         lds_wait(va);
 #pragma unroll
-        for (int i = 0; i < NDW; i++) {
+        for (int i = 0; i < NDT; i++) {
             oacc[i] = mfma16<T>(va[i], ph, oacc[i]);
             if constexpr (SPLITP) oacc[i] = mfma16<T>(va[i], pl, oacc[i]);
         }
@@ -983,20 +974,17 @@ __global__ __launch_bounds__(CW * 64, 1) void decode_block_kernel(
     const int64_t u = (int64_t)b * n_units + unit;
     if (splits == 1) {
 #pragma unroll
-        for (int i = 0; i < NDW; i++)
-            store_split<D>(oacc[i], m_run, l_part, (wave * NDW + i) * 4 + kg, n16, b, split, splits,
+        for (int i = 0; i < NDT; i++)
+            store_split<D>(oacc[i], m_run, l_part, i * 4 + kg, n16, b, split, splits,
                            gt, n_head, head0, u, gt * D, out, ws_ml, ws_acc);
     } else {
         float *ap = ws_acc + (u * splits + split) * (gt * D) + n16 * D + kg * 4;
 #pragma unroll
-        for (int i = 0; i < NDW; i++) *(f32x4 *)(ap + (wave * NDW + i) * 16) = oacc[i];
-        if (wave == 0 && kg == 0)
+        for (int i = 0; i < NDT; i++) *(f32x4 *)(ap + i * 16) = oacc[i];
+        if (kg == 0)
             *(float2 *)(ws_ml + ((u * splits + split) * gt + n16) * 2) = float2{m_run, l_part};
     }
 }
-
-// CW > 1 instances of decode_block_kernel exist for f16/bf16 caches only.
-template <class T> using MaybeF16 = typename std::conditional<__is_same(T, F32), F16, T>::type;
 
 constexpr int kMaxSplits = 256;
 
@@ -1100,11 +1088,9 @@ struct MfmaPlan {
 
 static const int kEnvMw = env_override("ULLM_HIP_DECODE_MW");
 static const int kEnvSplitsM = env_override("ULLM_HIP_DECODE_SPLITS");
-// Tuning overrides: ULLM_HIP_DECODE_NOBLOCK=1 runs one-block splits on
-// decode_dma_kernel instead of decode_block_kernel; ULLM_HIP_DECODE_CW=2/4
-// shares each block among that many waves.
+// Tuning override: ULLM_HIP_DECODE_NOBLOCK=1 runs one- and two-block splits
+// on decode_dma_kernel instead of decode_block_kernel.
 static const bool kNoBlock = env_override("ULLM_HIP_DECODE_NOBLOCK") == 1;
-static const int kEnvCw = env_override("ULLM_HIP_DECODE_CW");
 
 static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_len, int window,
                           bool paged = false) {
@@ -1276,7 +1262,7 @@ static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const
     const int fetch_len = batch == 1 && (win <= 0 || max_len <= win) ? max_len : 0;
     if constexpr (D > 128) {
         if (p.kb == 16) {
-            hipLaunchKernelGGL((decode_block_kernel<T, D, 1, 1, 16>), dim3(p.splits, p.n_units, batch),
+            hipLaunchKernelGGL((decode_block_kernel<T, D, 1, 16>), dim3(p.splits, p.n_units, batch),
                                dim3(64), 0, st, q, (const char *)kc, (const char *)vc, kvs, ss, lens,
                                win, fetch_len, nh, kv_mul, p.gt, p.n_units, p.chunk, p.splits, qs,
                                out, (float *)(ws + p.off_ml), (float *)(ws + p.off_acc));
@@ -1285,16 +1271,14 @@ static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const
         }
     } else {
         if (p.mw == 1 && (p.chunk == kTok || p.chunk == 2 * kTok) && p.splits > 1 && !kNoBlock) {
-            auto go = [&](auto kern, int cw) {
-                hipLaunchKernelGGL(kern, dim3(p.splits, p.n_units, batch), dim3(cw * 64), 0, st, q, (const char *)kc, (const char *)vc, kvs, ss,
-                               lens, win, fetch_len, nh, kv_mul, p.gt, p.n_units, p.chunk,
-                               p.splits, qs, out, (float *)(ws + p.off_ml),
-                               (float *)(ws + p.off_acc));
+            auto go = [&](auto kern) {
+                hipLaunchKernelGGL(kern, dim3(p.splits, p.n_units, batch), dim3(64), 0, st, q,
+                                   (const char *)kc, (const char *)vc, kvs, ss, lens, win,
+                                   fetch_len, nh, kv_mul, p.gt, p.n_units, p.chunk, p.splits, qs,
+                                   out, (float *)(ws + p.off_ml), (float *)(ws + p.off_acc));
             };
-            if (p.chunk == 2 * kTok) go(decode_block_kernel<T, D, 1, 2>, 1);
-            else if (!__is_same(T, F32) && kEnvCw == 2) go(decode_block_kernel<MaybeF16<T>, D, 2, 1>, 2);
-            else if (!__is_same(T, F32) && kEnvCw == 4) go(decode_block_kernel<MaybeF16<T>, D, 4, 1>, 4);
-            else go(decode_block_kernel<T, D, 1, 1>, 1);
+            if (p.chunk == 2 * kTok) go(decode_block_kernel<T, D, 2>);
+            else go(decode_block_kernel<T, D, 1>);
             launch_merge<D>(p, batch, nh, out, ws, st);
             return;
         }
