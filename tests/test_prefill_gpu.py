@@ -117,6 +117,33 @@ def test_head_dim_256_geometries(dev, dtype, S, H, Hk, start_pos, window):
     run_case(dev, dtype, S, H, Hk, 256, start_pos=start_pos, window=window, seed=12)
 
 
+def prefill128_kernel(S, H, Hk, start_pos=0, window=0):
+    """Which kernel a head_dim-128 prompt runs: prefill16 when prefill4's
+    causal pairs would be 128 or fewer (the rule in prefill.hip), restated."""
+    kv_mul = H // Hk
+    hw = 4 if kv_mul % 4 == 0 else (2 if kv_mul % 2 == 0 else 1)
+    ng = (S + 32 * (4 // hw) - 1) // (32 * (4 // hw))
+    pairs = (H // kv_mul) * (kv_mul // hw) * ((ng + 1) // 2)
+    paired = not (0 < window < start_pos + S)
+    return "prefill16" if paired and pairs <= 128 else ("prefill4" if paired else "prefill2")
+
+
+# head_dim 128 on both sides of the prefill16 / prefill4 rule, with a
+# chunk's start_pos and a GQA ratio that is not a power of two.
+P128_CASES = [("bf16", 2048, 12, 2, 0), ("f16", 1024, 32, 8, 0), ("bf16", 1536, 32, 8, 0),
+              ("f16", 777, 16, 2, 100), ("bf16", 300, 6, 2, 0), ("f16", 2048, 32, 8, 0)]
+
+
+@pytest.mark.parametrize("dtype,S,H,Hk,start_pos", P128_CASES)
+def test_head_dim_128_both_kernels(dev, dtype, S, H, Hk, start_pos):
+    run_case(dev, dtype, S, H, Hk, 128, start_pos=start_pos, seed=21)
+
+
+def test_head_dim_128_cases_cover_both_kernels():
+    seen = {prefill128_kernel(S, H, Hk, sp) for (_, S, H, Hk, sp) in P128_CASES}
+    assert {"prefill16", "prefill4"} <= seen, seen
+
+
 def test_head_dim_256_geometries_covered():
     """The cases above reach both key-stream counts with 4, 2 and 1 heads per
     workgroup, and the value split with two key streams at each head count."""
