@@ -723,7 +723,8 @@ def main():
         "f32_prefill": {"workload": "cfg3 shape (S=2048, 32/8 heads, head_dim 128) over an f32 "
                                     "cache, the reference's own cache dtype: Q.K on bf16 hi + lo "
                                     "halves of Q and K, P.V in f16",
-                        "kernel": "prefill_f32_kernel<128>",
+                        "kernel": "prefill16_kernel<F32,KS,1,128> (f32 tiles by LDS DMA, "
+                                  "split in LDS into bf16 hi/lo K and f16 V)",
                         "ms": round(res["f32_prefill"]["ms"], 4),
                         "tflops": round(res["f32_prefill"]["tflops"], 2),
                         "frac_mfma": round(res["f32_prefill"]["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),

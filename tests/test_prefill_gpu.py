@@ -246,6 +246,22 @@ def test_f32_cache_workgroup_geometries(dev, H, Hk, D, S, start_pos, window):
             rows=list(range(S)))
 
 
+# The f32 cache at head_dim 128 runs prefill16_kernel's f32 mode: its
+# one- and two-stream geometries with 4, 2 and 1 heads per workgroup.
+F32_P16_CASES = [(2048, 16, 8, 0, 0), (3000, 12, 4, 0, 0), (2048, 16, 8, 64, 500),
+                 (1100, 32, 4, 0, 0), (400, 12, 4, 10, 0), (513, 8, 2, 0, 0)]
+
+
+@pytest.mark.parametrize("S,H,Hk,start_pos,window", F32_P16_CASES)
+def test_f32_cache_prefill16_geometries(dev, S, H, Hk, start_pos, window):
+    run_f32(dev, S, H, Hk, 128, start_pos=start_pos, window=window, seed=26)
+
+
+def test_f32_cache_geometries_covered():
+    seen = {p16_geometry(S, H, Hk, sp, w)[:2] for (S, H, Hk, sp, w) in F32_P16_CASES}
+    assert {(1, 4), (1, 2), (1, 1), (2, 4), (2, 2), (2, 1)} <= seen, seen
+
+
 def test_cfg3_pipeline_norm_rope_all_rows(dev):
     """cfg3 as BASELINE configures it, end to end at full size: raw f32 Q/K/V
     ~ N(0,1) -> fused append (per-head RMSNorm with unit weights, eps 1e-6,

@@ -1609,6 +1609,12 @@ extern "C" int ullm_hip_attn_prefill(const void *q, const void *k_cache, const v
     const int kv_mul = n_head / n_kv_head;
     hipStream_t st = (hipStream_t)stream;
     if (dtype == ULLM_DT_F32) {
+        // head_dim 128: prefill16_kernel's f32 mode (faster at every measured
+        // prompt, 128..4096 rows); ULLM_HIP_PREFILL_F32=4 keeps prefill_f32_kernel.
+        static const int ef = env_override("ULLM_HIP_PREFILL_F32");
+        if (head_dim == 128 && ef != 4)
+            return launch_prefill16_128(ULLM_DT_F32, q, k_cache, v_cache, kv_stride, S, start_pos, window,
+                                        n_head, kv_mul, qs, out, st, KvPages{});
         if (head_dim == 64)
             return launch_prefill_f32<64>(q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);
         return launch_prefill_f32<128>(q, k_cache, v_cache, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st);

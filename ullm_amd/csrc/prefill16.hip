@@ -65,14 +65,15 @@ __device__ __forceinline__ int p16_vswz(int r) { return ((r & 7) << 1) | ((r >> 
 
 // Ring stages per key stream: as many K/V stages as a workgroup's share of
 // 160 KB holds (OCC workgroups per CU), at most 4.
-template <int KS, int DS, int D, int OCC>
+template <int KS, int DS, int D, int OCC, int EB = 2>
 constexpr int p16_stages() {
-    constexpr int st = 160 * 1024 / OCC / (KS * (32 * D * 2 + 32 * D * 2 / DS));
+    constexpr int stage = EB == 4 ? 2 * 32 * D * 4 : 32 * D * 2 + 32 * D * 2 / DS;
+    constexpr int st = 160 * 1024 / OCC / (KS * stage);
     return st > 4 ? 4 : st;
 }
 
 template <class T, int KS, int DS, int D = 256, int OCC = 1,
-          int NSTG = p16_stages<KS, DS, D, OCC>()>
+          int NSTG = p16_stages<KS, DS, D, OCC, T::bytes>()>
 __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
     const uint16_t *__restrict__ q, const char *__restrict__ kc, const char *__restrict__ vc,
     int64_t kv_stride, int S, int start_pos, int window, int n_head, int kv_mul, int hw,
@@ -80,12 +81,24 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
     // DS = 2: the workgroup computes the full Q.K and softmax of its rows but
     // P.V and the output for one half of the 256 value columns only; its V
     // tiles hold that half (256-byte rows).
-    constexpr int BN = 32, RB = D * 2, RBV = RB / DS;
+    // T = F32 (the reference's cache dtype, head_dim 128): K and V tiles
+    // arrive in f32 and each wave converts the chunks its own DMA wrote, in
+    // place, into bf16 hi and lo K tiles and an f16 V tile laid out as the
+    // 16-bit path's; Q.K = Khi.Qhi + Khi.Qlo + Klo.Qhi (about 2^-16 of each
+    // product), P.V as for f16.
+    constexpr bool F = __is_same(T, F32);
+    using MT = typename std::conditional<F, BF16, T>::type;  // Q.K operand type
+    constexpr int BN = 32, RB = D * 2, RBV = RB / DS;  // rows of the 16-bit tiles
     static_assert(D == 128 || D == 256, "head_dim");
-    constexpr int TILE = BN * RB, TILEV = BN * RBV, STAGE = TILE + TILEV;
+    static_assert(!F || (D == 128 && DS == 1), "f32 cache: head_dim 128, no value split");
+    constexpr int RBF = D * T::bytes;  // cache bytes per key row of one head
+    constexpr int TILE = BN * RB, TILEV = BN * RBV;
+    constexpr int DMAK = F ? BN * RBF : TILE, DMAV = F ? BN * RBF : TILEV;  // bytes fetched
+    constexpr int STAGE = DMAK + DMAV;
+    constexpr int VOFF = F ? 2 * TILE : TILE;  // V tile in a stage (f32: after K hi, K lo)
     constexpr int NW = 8, NWS = NW / KS;  // waves per stream
-    constexpr int NIC = TILE / 1024 / NWS;    // 1 KiB DMA chunks per wave, K
-    constexpr int NICV = TILEV / 1024 / NWS;  // and V
+    constexpr int NIC = DMAK / 1024 / NWS;    // 1 KiB DMA chunks per wave, K
+    constexpr int NICV = DMAV / 1024 / NWS;  // and V
     constexpr int NKS = D / 32, NDT = D / 16 / DS;  // Q k-steps; value d tiles of this workgroup
     constexpr bool CVTV = __is_same(T, BF16);
     constexpr float kLazy = 8.0f;
@@ -127,29 +140,39 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
     const int tbase = t0 + ks * nsteps;  // this stream's first tile
 
     // ---- K/V DMA: 1 KiB chunks = two key rows, lane -> (row, slot) ----
-    const int rbg = (int)(kv_stride * 2);
+    const int rbg = (int)(kv_stride * T::bytes);
     // Contiguous cache: one resource over the layer (the entry point bounds it
     // below 2 GiB).  Paged: resources per tile from page_tile; a zero-range
     // resource for the steps past the unit's range.
-    const int range = pgs.tab ? 0 : (kv_len - 1) * rbg + D * 2;
+    const int range = pgs.tab ? 0 : (kv_len - 1) * rbg + RBF;
     const __amdgpu_buffer_rsrc_t krs =
-        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + (int64_t)kvh * RBF), 0, range, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t vrs =
-        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + (int64_t)kvh * D * 2), 0, range, kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + (int64_t)kvh * RBF), 0, range, kRsrcWord3);
     int kofs[NIC], vofs[NICV];
 #pragma unroll
     for (int i = 0; i < NIC; i++) {
-        constexpr int KSL = RB / 16;  // 16-byte slots per K row
-        const int r = (ws * NIC + i) * (1024 / RB) + lane / KSL;
-        kofs[i] = r * rbg + (((lane % KSL) ^ p16_kswz(r)) * 16);
+        if constexpr (F) {  // f32 staging: plain rows, read back by the lane that fetched them
+            const int r = (ws * NIC + i) * (1024 / RBF) + lane / (RBF / 16);
+            kofs[i] = r * rbg + (lane % (RBF / 16)) * 16;
+        } else {
+            constexpr int KSL = RB / 16;  // 16-byte slots per K row
+            const int r = (ws * NIC + i) * (1024 / RB) + lane / KSL;
+            kofs[i] = r * rbg + (((lane % KSL) ^ p16_kswz(r)) * 16);
+        }
     }
     // A V chunk is 1024 / RBV rows; slot c of row r takes the row's value
     // chunk (c ^ p16_vswz(r)) of half dh.
     constexpr int VSL = RBV / 16;  // 16-byte slots per V row
 #pragma unroll
     for (int i = 0; i < NICV; i++) {
-        const int r = (ws * NICV + i) * (1024 / RBV) + lane / VSL;
-        vofs[i] = r * rbg + ((((lane % VSL) ^ p16_vswz(r)) + dh * VSL) * 16);
+        if constexpr (F) {
+            const int r = (ws * NICV + i) * (1024 / RBF) + lane / (RBF / 16);
+            vofs[i] = r * rbg + (lane % (RBF / 16)) * 16;
+        } else {
+            const int r = (ws * NICV + i) * (1024 / RBV) + lane / VSL;
+            vofs[i] = r * rbg + ((((lane % VSL) ^ p16_vswz(r)) + dh * VSL) * 16);
+        }
     }
     char *const ring = lds + ks * NSTG * STAGE;
     auto issue = [&](int j) {  // step j's tile of this stream into stage j % NSTG
@@ -164,11 +187,42 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
         for (int i = 0; i < NIC; i++) dma16(kr, st + (ws * NIC + i) * 1024, kofs[i] + so, 0);
 #pragma unroll
         for (int i = 0; i < NICV; i++)
-            dma16(vr, st + TILE + (ws * NICV + i) * 1024, vofs[i] + so, 0);
+            dma16(vr, st + DMAK + (ws * NICV + i) * 1024, vofs[i] + so, 0);
     };
-    // bf16 V -> f16 in place, for the chunks this wave's DMA wrote.
+    // bf16 V -> f16 in place, for the chunks this wave's DMA wrote; f32 K and
+    // V -> bf16 hi/lo K and f16 V tiles (every wave reads its f32 chunks,
+    // a barrier, then the converted writes: they land on other waves' rows).
     auto widen = [&](int stg) {
-        if constexpr (CVTV) {
+        if constexpr (F) {
+            const uint32_t base = lds_addr(ring + stg * STAGE);
+            u32x4 kx[NIC], vx[NICV];
+#pragma unroll
+            for (int i = 0; i < NIC; i++) kx[i] = lds_read_b128(base + (ws * NIC + i) * 1024 + lane * 16);
+#pragma unroll
+            for (int i = 0; i < NICV; i++)
+                vx[i] = lds_read_b128(base + DMAK + (ws * NICV + i) * 1024 + lane * 16);
+            lds_wait_any();
+            asm volatile("s_barrier" ::: "memory");
+            constexpr int FSL = RBF / 16;  // f32 slots per row: four elements each
+#pragma unroll
+            for (int i = 0; i < NIC; i++) {
+                tie(kx[i]);
+                const int r = (ws * NIC + i) * (1024 / RBF) + lane / FSL, sl = lane % FSL;
+                const u32x2 a = split2<BF16>(__uint_as_float(kx[i][0]), __uint_as_float(kx[i][1]));
+                const u32x2 b = split2<BF16>(__uint_as_float(kx[i][2]), __uint_as_float(kx[i][3]));
+                const uint32_t o = base + r * RB + (((sl >> 1) ^ p16_kswz(r)) * 16) + (sl & 1) * 8;
+                lds_write_b64(o, u32x2{a[0], b[0]});
+                lds_write_b64(o + TILE, u32x2{a[1], b[1]});
+            }
+#pragma unroll
+            for (int i = 0; i < NICV; i++) {
+                tie(vx[i]);
+                const int r = (ws * NICV + i) * (1024 / RBF) + lane / FSL, sl = lane % FSL;
+                const uint32_t o = base + VOFF + r * RBV + (((sl >> 1) ^ p16_vswz(r)) * 16) + (sl & 1) * 8;
+                lds_write_b64(o, u32x2{pack_f16x2(__uint_as_float(vx[i][0]), __uint_as_float(vx[i][1])),
+                                       pack_f16x2(__uint_as_float(vx[i][2]), __uint_as_float(vx[i][3]))});
+            }
+        } else if constexpr (CVTV) {
             const uint32_t vb = lds_addr(ring + stg * STAGE + TILE + ws * NICV * 1024) + lane * 16;
             u32x4 w[NICV];
 #pragma unroll
@@ -200,11 +254,12 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
             const int ch = 2 * dt + ((r16 & 3) >> 1);
-            va[dt] = TILE + vr * RBV + ((ch ^ p16_vswz(vr)) * 16) + 8 * (r16 & 1);
+            va[dt] = VOFF + vr * RBV + ((ch ^ p16_vswz(vr)) * 16) + 8 * (r16 & 1);
         }
     }
 
     u32x4 qreg[NKS];  // Q^T operand: row r16, d = 32 s + 8 g .. +7
+    u32x4 qlo[F ? NKS : 1];  // f32: the lo halves
     f32x4 oacc[NDT];
 #pragma unroll
     for (int i = 0; i < NDT; i++) oacc[i] = f32x4{};
@@ -230,10 +285,11 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
         for (int i = 0; i < 4; i++) kaddr[i] = sb + ka[i];
 #pragma unroll
         for (int i = 0; i < 8; i++) vaddr[i] = sb + va[i];
-        u32x4 kb[2 * NKS];
+        u32x4 kb[2 * NKS], kl[F ? 2 * NKS : 1];
         static_for<0, 2 * NKS>([&](auto ic) {
             constexpr int idx = decltype(ic)::value, s = idx >> 1, kt = idx & 1;
             kb[idx] = lds_read_b128_at<(s >> 2) * 256 + kt * 16 * RB>(kaddr[s & 3]);
+            if constexpr (F) kl[idx] = lds_read_b128_at<TILE + (s >> 2) * 256 + kt * 16 * RB>(kaddr[s & 3]);
         });
         u32x4 vb[NDT];
         auto rdv = [&](auto dtc) {
@@ -242,6 +298,19 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
             const u32x2 hi = lds_read_tr16_b64_at<(dt >> 3) * 256 + 16 * RBV>(vaddr[dt & 7]);
             vb[dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         };
+        if constexpr (F) {
+            lds_wait_any();  // every K hi and lo read; then all V^T reads under the MFMAs
+            rdv(Int<0>{}); rdv(Int<1>{}); rdv(Int<2>{}); rdv(Int<3>{});
+            rdv(Int<4>{}); rdv(Int<5>{}); rdv(Int<6>{}); rdv(Int<7>{});
+            static_for<0, 2 * NKS>([&](auto ic) {
+                constexpr int idx = decltype(ic)::value, s = idx >> 1, kt = idx & 1;
+                tie(kb[idx]);
+                tie(kl[idx]);
+                sacc[kt] = mfma16<MT>(kb[idx], qreg[s], sacc[kt]);
+                sacc[kt] = mfma16<MT>(kb[idx], qlo[s], sacc[kt]);
+                sacc[kt] = mfma16<MT>(kl[idx], qreg[s], sacc[kt]);
+            });
+        } else {
         lds_wait_n<NKS>();  // the first half of the K reads
         static_for<0, 2 * NKS>([&](auto ic) {
             constexpr int idx = decltype(ic)::value, s = idx >> 1, kt = idx & 1;
@@ -251,6 +320,7 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
             if constexpr (idx == 0) { rdv(Int<0>{}); rdv(Int<1>{}); rdv(Int<2>{}); rdv(Int<3>{}); }
             if constexpr (idx == NKS) { rdv(Int<4>{}); rdv(Int<5>{}); rdv(Int<6>{}); rdv(Int<7>{}); }
         });
+        }
         // Mask where the tile reaches past the wave's first row or before the
         // window of its last (wave-uniform test): key - pos_row must lie in
         // (dlo, 0].  The scale is applied inside the exponent (qscale > 0, so
@@ -317,19 +387,46 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
     // Q goes out after the first tile, as untracked loads: the loop's first
     // wait (later tiles left in flight) covers it.
     issue(0);
+    u32x4 qf[F ? 2 * NKS : 1];  // f32: raw q, split after it lands
     {
-        const i32x4 qrs = raw_rsrc(q, (int)((int64_t)S * q_dim * 2));
-        const int qo = qrow < S ? (int)(((int64_t)qrow * q_dim + (int64_t)head * D + g * 8) * 2)
+        const i32x4 qrs = raw_rsrc(q, (int)((int64_t)S * q_dim * T::bytes));
+        const int qo = qrow < S ? (int)(((int64_t)qrow * q_dim + (int64_t)head * D + g * 8) * T::bytes)
                                 : 0x7ffffff0;  // past the range: zeros
 #pragma unroll
-        for (int s = 0; s < NKS; s++) qreg[s] = buffer_load_b128_untracked(qrs, qo + s * 64);
+        for (int s = 0; s < NKS; s++) {
+            if constexpr (F) {
+                qf[2 * s] = buffer_load_b128_untracked(qrs, qo + s * 128);
+                qf[2 * s + 1] = buffer_load_b128_untracked(qrs, qo + s * 128 + 16);
+            } else {
+                qreg[s] = buffer_load_b128_untracked(qrs, qo + s * 64);
+            }
+        }
     }
 #pragma unroll
     for (int j = 1; j < NSTG - 1; j++) issue(j);
+    if constexpr (F) {  // q landed with tile 0 (issued before tiles 1..): split it
+        __builtin_amdgcn_s_waitcnt(vm_wait((NSTG - 2) * (NIC + NICV)));
+#pragma unroll
+        for (int s = 0; s < NKS; s++) {
+            tie(qf[2 * s]);
+            tie(qf[2 * s + 1]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const u32x4 &src = e < 2 ? qf[2 * s] : qf[2 * s + 1];
+                const u32x2 hl = split2<BF16>(__uint_as_float(src[(2 * e) & 3]),
+                                              __uint_as_float(src[(2 * e + 1) & 3]));
+                qreg[s][e] = hl[0];
+                qlo[s][e] = hl[1];
+            }
+        }
+    }
     for (int j = 0; j < nsteps; j++) {
         __builtin_amdgcn_s_waitcnt(vm_wait((NSTG - 2) * (NIC + NICV)));
 #pragma unroll
-        for (int s = 0; s < NKS; s++) tie(qreg[s]);
+        for (int s = 0; s < NKS; s++) {
+            tie(qreg[s]);
+            if constexpr (F) tie(qlo[s]);
+        }
         widen(j % NSTG);
         lds_wait_any();
         asm volatile("s_barrier" ::: "memory");
@@ -437,7 +534,8 @@ int launch_prefill16(int dtype, const void *q, const void *kc, const void *vc, i
     return check_hip(hipGetLastError(), "prefill (16-row waves) launch");
 }
 
-// head_dim 128 on prefill16_kernel (short prompts; no value split).
+// head_dim 128 on prefill16_kernel (short prompts; no value split), bf16,
+// f16 or f32 cache (contiguous only for f32).
 int launch_prefill16_128(int dtype, const void *q, const void *kc, const void *vc, int64_t kvs,
                          int S, int start_pos, int window, int n_head, int kv_mul, float qs,
                          float *out, hipStream_t st, KvPages pgs) {
@@ -457,6 +555,7 @@ int launch_prefill16_128(int dtype, const void *q, const void *kc, const void *v
         else go(prefill16_kernel<T, 1, 1, 128, 1>);
     };
     if (dtype == ULLM_DT_BF16) pick(BF16{});
+    else if (dtype == ULLM_DT_F32) pick(F32{});
     else pick(F16{});
     return check_hip(hipGetLastError(), "prefill (16-row waves, head_dim 128) launch");
 }
