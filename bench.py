@@ -685,7 +685,7 @@ def main():
                               "tflops": round(res["cfg3_paged"]["tflops"], 2)}},
         "cfg1_decode": {"workload": "cfg1 Llama-3.2-1B-shaped decode: 32/8 heads, head_dim 64, "
                                     "f32 KV 512, 28 layers per graph (rotated past the MALL)",
-                        "kernel": "decode_block_kernel<F32,64,1,1> (bf16 hi + lo MFMA) + "
+                        "kernel": "decode_block_kernel<F32,64,1,32> (bf16 hi + lo MFMA) + "
                                   "decode_merge_kernel",
                         "us_per_layer": round(c1["us_per_layer"], 3),
                         "algorithmic_bytes": int(c1["layer_bytes"]),
@@ -695,7 +695,7 @@ def main():
                                     "256, f16 KV, context 8192; 6 layers per step = 5 sliding-"
                                     "window layers (1024 keys) + 1 global layer, rotated past "
                                     "the MALL",
-                        "kernel": "window layers decode_block_kernel<F16,256,1,1,16>, global layer "
+                        "kernel": "window layers decode_block_kernel<F16,256,1,16>, global layer "
                                   "decode_mfma_kernel<F16,256,false,4>; each + decode_merge_kernel",
                         "us_per_group": round(c4["ms_per_step"] * 1e3, 3),
                         "us_per_layer": round(c4["us_per_layer"], 3),
@@ -775,7 +775,7 @@ def main():
                      "frac": round(d["gbps_step"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("bytes_per_launch") if traffic else None,
                      "traffic_measured_at": traffic.get("commit") if traffic else None,
-                     "kernel": "decode_block_kernel<F16,128,1,1> + decode_merge_kernel<128,4,2,256> "
+                     "kernel": "decode_block_kernel<F16,128,1,32> + decode_merge_kernel<128,4,2,256> "
                                "(one decode-attention op per layer)",
                      "algorithmic_bytes": int(d["layer_bytes"]),
                      "us_per_launch": round(d["us_per_layer"], 3),
