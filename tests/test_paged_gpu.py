@@ -252,6 +252,9 @@ PREFILL_CASES = [
     (2048, 0, 32, 8, 128, "bf16", 256, 0),      # cfg3 shape
     (1024, 0, 8, 4, 256, "f16", 64, 0),         # head_dim 256 (split-K kernel), cfg4 shape
     (300, 900, 8, 4, 256, "bf16", 128, 500),    # head_dim 256, chunked, binding window
+    (300, 0, 8, 2, 128, "f32", 64, 0),          # f32 pages (prefill16's f32 mode), two key streams
+    (2048, 0, 32, 8, 128, "f32", 256, 0),       # f32, cfg3 shape, one key stream
+    (200, 700, 12, 4, 128, "f32", 128, 250),    # f32, chunked, binding window, 1 head per workgroup
 ]
 
 

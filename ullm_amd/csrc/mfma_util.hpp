@@ -202,8 +202,8 @@ struct KvPages {
 };
 
 // Buffer resources and scalar offset of the key tile starting at key0 (a
-// tile never crosses a page).
-template <int D>
+// tile never crosses a page).  EB: bytes per cache element.
+template <int D, int EB = 2>
 __device__ __forceinline__ void page_tile(const KvPages &pg, const char *kc, const char *vc,
                                           int kvh, int rbg, int kv_len, int key0,
                                           __amdgpu_buffer_rsrc_t &kr, __amdgpu_buffer_rsrc_t &vr,
@@ -211,9 +211,9 @@ __device__ __forceinline__ void page_tile(const KvPages &pg, const char *kc, con
     const int pi = key0 >> pg.shift;
     const int phys = key0 < kv_len && pi < pg.tab_len ? pg.tab[pi] : -1;
     const bool ok = phys >= 0 && phys < pg.n_pages;
-    const int64_t pb = ((int64_t)(ok ? phys : 0) << pg.shift) * rbg + (int64_t)kvh * D * 2;
+    const int64_t pb = ((int64_t)(ok ? phys : 0) << pg.shift) * rbg + (int64_t)kvh * D * EB;
     const int rows = min(1 << pg.shift, kv_len - (pi << pg.shift));
-    const int range = ok ? (rows - 1) * rbg + D * 2 : 0;
+    const int range = ok ? (rows - 1) * rbg + D * EB : 0;
     kr = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + pb), 0, range, kRsrcWord3);
     vr = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vc + pb), 0, range, kRsrcWord3);
     so = __builtin_amdgcn_readfirstlane((key0 & ((1 << pg.shift) - 1)) * rbg);

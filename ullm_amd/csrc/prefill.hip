@@ -1630,20 +1630,22 @@ extern "C" int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, c
                                            int table_len, int S, int start_pos, int window,
                                            int n_head, int n_kv_head, int head_dim, float scale,
                                            float *out, void *stream) {
-    if (dtype != ULLM_DT_F16 && dtype != ULLM_DT_BF16)
-        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: dtype %d (f16/bf16)", dtype);
+    if (dtype != ULLM_DT_F16 && dtype != ULLM_DT_BF16 && !(dtype == ULLM_DT_F32 && head_dim == 128))
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: dtype %d at head_dim %d (f16/bf16; f32 at 128)",
+                         dtype, head_dim);
     if (head_dim != 64 && head_dim != 128 && head_dim != 256)
         return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: head_dim %d not in {64,128,256}", head_dim);
     if (n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || S < 0 || start_pos < 0)
         return set_error(ULLM_HIP_E_INVALID, "prefill_paged: bad shape S=%d start_pos=%d heads=%d/%d",
                          S, start_pos, n_head, n_kv_head);
-    if (kv_stride < (int64_t)n_kv_head * head_dim || (kv_stride * 2) % 16)
+    const int eb = dtype_bytes(dtype);
+    if (kv_stride < (int64_t)n_kv_head * head_dim || (kv_stride * eb) % 16)
         return set_error(ULLM_HIP_E_INVALID,
                          "prefill_paged: kv_stride must be >= n_kv_head*head_dim and 16-byte aligned");
     if (page_size < 64 || (page_size & (page_size - 1)))
         return set_error(ULLM_HIP_E_INVALID, "prefill_paged: page_size %d must be a power of two >= 64",
                          page_size);
-    if ((int64_t)page_size * kv_stride * 2 > 0x7fff0000LL)
+    if ((int64_t)page_size * kv_stride * eb > 0x7fff0000LL)
         return set_error(ULLM_HIP_E_INVALID, "prefill_paged: a page exceeds 2 GiB");
     if (n_pages < 1) return set_error(ULLM_HIP_E_INVALID, "prefill_paged: n_pages %d < 1", n_pages);
     if ((int64_t)table_len * page_size < (int64_t)start_pos + S)
@@ -1658,6 +1660,9 @@ extern "C" int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, c
     const float qs = scale * kLog2e;
     const int kv_mul = n_head / n_kv_head;
     hipStream_t st = (hipStream_t)stream;
+    if (dtype == ULLM_DT_F32)  // f32 pages: prefill16_kernel's f32 mode
+        return launch_prefill16_128(ULLM_DT_F32, q, k_pages, v_pages, kv_stride, S, start_pos, window,
+                                    n_head, kv_mul, qs, out, st, pgs);
     if (dtype == ULLM_DT_BF16) {
         if (head_dim == 64) PrefillLaunch<BF16, 64>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
         else if (head_dim == 128) PrefillLaunch<BF16, 128>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);

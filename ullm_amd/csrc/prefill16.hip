@@ -180,7 +180,7 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
         const bool live = j < nsteps && t < t1;
         __amdgpu_buffer_rsrc_t kr = krs, vr = vrs;
         int so;
-        if (pgs.tab && live) page_tile<D>(pgs, kc, vc, kvh, rbg, kv_len, t * BN, kr, vr, so);
+        if (pgs.tab && live) page_tile<D, T::bytes>(pgs, kc, vc, kvh, rbg, kv_len, t * BN, kr, vr, so);
         else so = __builtin_amdgcn_readfirstlane(live ? t * BN * rbg : range);  // range 0 if paged
         char *st = ring + (j % NSTG) * STAGE;
 #pragma unroll
@@ -535,7 +535,7 @@ int launch_prefill16(int dtype, const void *q, const void *kc, const void *vc, i
 }
 
 // head_dim 128 on prefill16_kernel (short prompts; no value split), bf16,
-// f16 or f32 cache (contiguous only for f32).
+// f16 or f32 cache, contiguous or paged.
 int launch_prefill16_128(int dtype, const void *q, const void *kc, const void *vc, int64_t kvs,
                          int S, int start_pos, int window, int n_head, int kv_mul, float qs,
                          float *out, hipStream_t st, KvPages pgs) {
