@@ -12,7 +12,6 @@
 //!
 //! Not compiled here: the build image of this repository has no cargo.
 //! Every call it makes is one the repository's tests drive through ctypes.
-use std::cell::RefCell;
 use std::os::raw::{c_int, c_void};
 
 use ullm_core::{Error, Result};
@@ -132,14 +131,11 @@ pub struct HipAttention {
     val_cache: DevBuf,
     rope_cs: DevBuf,
     /// 1..=n_ctx as i32, uploaded once: the decode at `pos` passes the device
-    /// address of entry `pos` (= pos + 1) as its seq_lens, and an f32-cache
-    /// prompt passes the s consecutive entries from its start, so no step
+    /// address of entry `pos` (= pos + 1) as its seq_lens, so no step
     /// uploads a length (and a captured step replays kernels only).
     lens: DevBuf,
     ws: DevBuf,
     ws_bytes: usize,
-    /// Workspace of the f32-cache prompt path (s ragged rows), grown on demand.
-    batch_ws: RefCell<Option<DevBuf>>,
     q: DevBuf,
     kv: DevBuf,
     out: DevBuf,
@@ -177,7 +173,6 @@ impl HipAttention {
             lens: DevBuf::from_slice(&lens)?,
             ws: DevBuf::zeroed(ws_bytes)?,
             ws_bytes,
-            batch_ws: RefCell::new(None),
             q: DevBuf::zeroed(p.n_ctx * q_dim * 4)?,
             kv: DevBuf::zeroed(2 * p.n_ctx * kv_dim * 4)?,
             out: DevBuf::zeroed(p.n_ctx * q_dim * 4)?,
@@ -255,11 +250,8 @@ impl HipAttention {
     /// lib.rs:1021-1087).  Returns [s][n_head*D] f32.
     ///  * f16/bf16 cache: q goes out in the cache dtype, then one causal
     ///    prefill launch on the matrix cores.
-    ///  * f32 cache (the reference's own), head_dim 64/128: q stays f32 and
-    ///    the f32 prefill kernel runs Q.K on bf16 hi + lo halves.
-    ///  * f32 cache, head_dim 256: the s query rows attend as s ragged
-    ///    "sequences" over the shared cache (seq_stride 0) with lengths
-    ///    1..=s, on the split-KV decode kernel.
+    ///  * f32 cache (the reference's own): q stays f32 and the prefill
+    ///    kernel runs Q.K on bf16 hi + lo halves.
     pub fn forward_batch(&self, layer: usize, qs: &[f32], ks: &[f32], vs: &[f32], s: usize,
                          hp: HeadParams) -> Result<Vec<f32>> {
         let (p, kd) = (&self.p, self.kv_dim);
@@ -270,46 +262,23 @@ impl HipAttention {
         self.kv.upload(ks, 0)?;
         self.kv.upload(vs, s * kd * 4)?;
         let off = self.layer_off(layer);
-        let f32_rows = p.kv_dtype == ffi::ULLM_DT_F32 && p.head_dim == 256;
-        if f32_rows {
-            self.append(layer, s, 0, hp, self.q.ptr, ffi::ULLM_DT_F32)?;
-            let need = unsafe {
-                ffi::ullm_hip_decode_workspace_bytes(s as c_int, p.n_head as c_int,
-                                                     p.n_kv_head as c_int, p.head_dim as c_int,
-                                                     s as c_int, self.window(layer))
-            };
-            let mut ws = self.batch_ws.borrow_mut();
-            if ws.as_ref().map_or(true, |b| b.bytes < need) {
-                *ws = Some(DevBuf::zeroed(need)?);
-            }
-            let w = ws.as_ref().unwrap();
-            ffi::check(unsafe {
-                ffi::ullm_hip_attn_decode(
-                    self.q.ptr.cast(), self.key_cache.at(off), self.val_cache.at(off),
-                    p.kv_dtype, kd as i64, 0, self.lens.ptr.cast(), s as c_int,
-                    self.window(layer), s as c_int, p.n_head as c_int, p.n_kv_head as c_int,
-                    p.head_dim as c_int, self.scale(), self.out.ptr.cast(), w.ptr, w.bytes,
-                    std::ptr::null_mut())
-            })?;
-        } else {
-            // 16-bit caches: q in the cache dtype goes to `out` and the
-            // attention writes its f32 rows to `q`.  An f32 cache: q is
-            // prepared in place in `q` and the attention writes `out`.
-            let q_prep = if p.kv_dtype == ffi::ULLM_DT_F32 { self.q.ptr } else { self.out.ptr };
-            let o_dst = if p.kv_dtype == ffi::ULLM_DT_F32 { self.out.ptr } else { self.q.ptr };
-            self.append(layer, s, 0, hp, q_prep, p.kv_dtype)?;
-            ffi::check(unsafe {
-                ffi::ullm_hip_attn_prefill(
-                    q_prep, self.key_cache.at(off), self.val_cache.at(off), p.kv_dtype,
-                    kd as i64, s as c_int, 0, self.window(layer), p.n_head as c_int,
-                    p.n_kv_head as c_int, p.head_dim as c_int, self.scale(), o_dst.cast(),
-                    std::ptr::null_mut())
-            })?;
-            if p.kv_dtype != ffi::ULLM_DT_F32 {
-                let mut o = vec![0f32; s * p.n_head * p.head_dim];
-                self.q.download(&mut o)?;
-                return Ok(o);
-            }
+        // 16-bit caches: q in the cache dtype goes to `out` and the
+        // attention writes its f32 rows to `q`.  An f32 cache: q is prepared
+        // in place in `q` and the attention writes `out`.
+        let q_prep = if p.kv_dtype == ffi::ULLM_DT_F32 { self.q.ptr } else { self.out.ptr };
+        let o_dst = if p.kv_dtype == ffi::ULLM_DT_F32 { self.out.ptr } else { self.q.ptr };
+        self.append(layer, s, 0, hp, q_prep, p.kv_dtype)?;
+        ffi::check(unsafe {
+            ffi::ullm_hip_attn_prefill(
+                q_prep, self.key_cache.at(off), self.val_cache.at(off), p.kv_dtype,
+                kd as i64, s as c_int, 0, self.window(layer), p.n_head as c_int,
+                p.n_kv_head as c_int, p.head_dim as c_int, self.scale(), o_dst.cast(),
+                std::ptr::null_mut())
+        })?;
+        if p.kv_dtype != ffi::ULLM_DT_F32 {
+            let mut o = vec![0f32; s * p.n_head * p.head_dim];
+            self.q.download(&mut o)?;
+            return Ok(o);
         }
         let mut o = vec![0f32; s * p.n_head * p.head_dim];
         self.out.download(&mut o)?;

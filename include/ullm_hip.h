@@ -117,10 +117,8 @@ size_t ullm_hip_decode_noalloc_max_bytes(void);
  * q:     [S][n_head*head_dim] in `dtype` (after Q-norm and RoPE)
  * cache: `dtype` (f16, bf16 or f32; the same dtype as q)
  * out:   [S][n_head*head_dim] f32
- * head_dim in {64, 128, 256}; an f32 cache (the reference's own cache dtype)
- * takes head_dim 64 or 128 (ULLM_HIP_E_UNSUPPORTED for 256: attend row by
- * row with ullm_hip_attn_decode, batch = S, seq_stride 0).  With an f32
- * cache Q.K runs on bf16 hi + lo halves of Q and K (~2^-16 per product) and
+ * head_dim in {64, 128, 256}, for every dtype.  With an f32 cache (the
+ * reference's own cache dtype) Q.K runs on bf16 hi + lo halves of Q and K (~2^-16 per product) and
  * V is rounded to f16.  For bf16 and f32 caches P.V runs in f16 (V is
  * converted to f16 on chip), so |V| must stay below 65504.  A layer's cache
  * must stay below 2 GiB. */
@@ -259,8 +257,8 @@ int ullm_hip_qkv_append_paged(const float *q_in, const float *k_in, const float 
  * ullm_hip_attn_prefill on the gathered cache: chunked prefill of a
  * sequence whose earlier positions are already in pages.  No counterpart in
  * the reference (contiguous cache, lib.rs:184-185).  page_size: a power of
- * two >= 64; head_dim 64, 128 or 256 with f16/bf16 pages, head_dim 128 with
- * f32 pages and f32 q (else ULLM_HIP_E_UNSUPPORTED).
+ * two >= 64; head_dim 64, 128 or 256 with f16/bf16 pages, head_dim 128 or
+ * 256 with f32 pages and f32 q (else ULLM_HIP_E_UNSUPPORTED).
  * Pages outside [0, n_pages) read as zeros. */
 int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, const void *v_pages,
                                 int dtype, int64_t kv_stride, int page_size, int n_pages,

@@ -56,8 +56,8 @@ int main(void) {
     CHECK(ullm_hip_attn_decode_noalloc(fq, fake, fake, ULLM_DT_BF16, 256, 0, fl, 32768, 0, 1,
                                        16, 1, 256, 0.1f, fo, NULL) == ULLM_HIP_E_WORKSPACE);
 
-    /* prefill: f32 at head_dim 256 is unsupported, bad heads invalid */
-    CHECK(ullm_hip_attn_prefill(fake, fake, fake, ULLM_DT_F32, 512, 16, 0, 0, 8, 2, 256, 0.1f, fo,
+    /* prefill: head_dim 96 is unsupported (any dtype), bad heads invalid */
+    CHECK(ullm_hip_attn_prefill(fake, fake, fake, ULLM_DT_F32, 512, 16, 0, 0, 8, 2, 96, 0.1f, fo,
                                 NULL) == ULLM_HIP_E_UNSUPPORTED);
     CHECK(ullm_hip_attn_prefill(fake, fake, fake, ULLM_DT_BF16, 256, 16, 0, 0, 8, 3, 128, 0.1f, fo,
                                 NULL) != ULLM_HIP_OK);

@@ -76,8 +76,12 @@ def test_decode_argument_validation():
 
 def test_prefill_and_append_validation():
     lib = L.lib()
-    # f32 caches take head_dim 64/128; 256 is unsupported
-    assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_F32, 512, 16, 0, 0, 8, 2, 256, 0.1,
+    # every dtype takes head_dim 64/128/256: an f32 cache at 256 passes the
+    # dtype checks and stops at the null pointers; head_dim 96 is unsupported
+    assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_F32, 1024, 16, 0, 0, 8, 2, 256, 0.1,
+                                     None, None) == L.E_INVALID
+    assert b"null" in lib.ullm_hip_last_error()
+    assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_F32, 512, 16, 0, 0, 8, 2, 96, 0.1,
                                      None, None) == L.E_UNSUPPORTED
     assert lib.ullm_hip_attn_prefill(None, None, None, 7, 256, 16, 0, 0, 8, 2, 128, 0.1,
                                      None, None) == L.E_UNSUPPORTED
@@ -195,7 +199,6 @@ def test_paged_prefill_validation():
         return f(*a.values())
 
     assert call(dt=L.DT_F32, d=64) == L.E_UNSUPPORTED   # f32 pages: head_dim 128 only
-    assert call(dt=L.DT_F32, d=256) == L.E_UNSUPPORTED
     assert call(dt=L.DT_F32) == L.E_INVALID              # accepted; then the null pointers
     assert call(dt=L.DT_F16, kvs=1028) == L.E_INVALID    # 2056-byte rows: not
     assert call(d=96) == L.E_UNSUPPORTED

@@ -255,6 +255,7 @@ PREFILL_CASES = [
     (300, 0, 8, 2, 128, "f32", 64, 0),          # f32 pages (prefill16's f32 mode), two key streams
     (2048, 0, 32, 8, 128, "f32", 256, 0),       # f32, cfg3 shape, one key stream
     (200, 700, 12, 4, 128, "f32", 128, 250),    # f32, chunked, binding window, 1 head per workgroup
+    (500, 300, 8, 4, 256, "f32", 64, 0),        # f32 at head_dim 256, chunked
 ]
 
 

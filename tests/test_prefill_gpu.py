@@ -185,13 +185,6 @@ def test_prefill_rows_match_decode_full_size(dev):
     assert_close(out[rows], dec.view(len(rows), -1).cpu().numpy(), what="prefill vs decode")
 
 
-def test_rejects_f32_head_dim_256(dev):
-    q = torch.zeros(4, 256, device=dev)
-    with pytest.raises(A.L.UllmHipError) as e:
-        A.attn_prefill(q, q, q, 1, 1, 256)
-    assert e.value.code == A.L.E_UNSUPPORTED
-
-
 def run_f32(dev, S, H, Hk, D, start_pos=0, window=0, seed=1, rows=None, qk_scale=1.0):
     """The f32-cache prefill (Q.K on bf16 hi + lo halves, V and P in f16)
     against the f32 oracle on the same f32 inputs (no input rounding)."""
@@ -215,7 +208,7 @@ def test_f32_cache_cfg3_shape(dev):
     run_f32(dev, 2048, 32, 8, 128, seed=21)
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("S,start_pos,window", [(1, 0, 0), (33, 0, 0), (300, 0, 0),
                                                  (200, 100, 0), (700, 0, 100)])
 def test_f32_cache_shapes(dev, D, S, start_pos, window):
@@ -223,10 +216,11 @@ def test_f32_cache_shapes(dev, D, S, start_pos, window):
             rows=list(range(S)))
 
 
-def test_f32_cache_sharp_scores(dev):
+@pytest.mark.parametrize("D", [128, 256])
+def test_f32_cache_sharp_scores(dev, D):
     """Scores three times sharper than N(0,1) Q/K give (std 9): Q.K in plain
     f16 or bf16 would miss the tolerance here; the hi + lo split does not."""
-    run_f32(dev, 512, 8, 2, 128, seed=23, rows=list(range(0, 512, 3)), qk_scale=3.0)
+    run_f32(dev, 512, 8, 2, D, seed=23, rows=list(range(0, 512, 3)), qk_scale=3.0)
 
 
 @pytest.mark.parametrize("H,Hk", [(6, 1), (8, 8), (10, 5)])
@@ -255,6 +249,14 @@ F32_P16_CASES = [(2048, 16, 8, 0, 0), (3000, 12, 4, 0, 0), (2048, 16, 8, 64, 500
 @pytest.mark.parametrize("S,H,Hk,start_pos,window", F32_P16_CASES)
 def test_f32_cache_prefill16_geometries(dev, S, H, Hk, start_pos, window):
     run_f32(dev, S, H, Hk, 128, start_pos=start_pos, window=window, seed=26)
+
+
+# head_dim 256 over an f32 cache: one key stream, the value columns split
+# over two workgroups, 4, 2 and 1 heads per workgroup; cfg4's shape.
+@pytest.mark.parametrize("S,H,Hk,start_pos,window", [
+    (1024, 8, 4, 0, 1024), (700, 16, 4, 100, 300), (257, 6, 2, 3, 0), (130, 4, 4, 0, 0)])
+def test_f32_cache_head_dim_256(dev, S, H, Hk, start_pos, window):
+    run_f32(dev, S, H, Hk, 256, start_pos=start_pos, window=window, seed=27)
 
 
 def test_f32_cache_geometries_covered():

@@ -367,31 +367,12 @@ class GpuAttention:
                                               0, self.device)
         # seq_lens for every position, uploaded once: decoding at pos passes
         # the device slice holding pos + 1 (no per-token copy or fill, nothing
-        # for a captured graph to replay but kernels), and an f32-cache prefill
-        # at start_pos passes the S consecutive lengths from start_pos + 1.
+        # for a captured graph to replay but kernels).
         self._lens = torch.arange(1, p.n_ctx + 1, dtype=torch.int32, device=self.device)
-        self._batch_ws = {}
-
-    def _rows_decode(self, layer, qr, start_pos, S):
-        """f32-cache prefill: the S query rows as S ragged "sequences" over the
-        shared cache (seq_stride 0), lengths start_pos + 1 .. start_pos + S."""
-        p = self.p
-        key = (S, start_pos + S, self._window(layer))
-        ws = self._batch_ws.get(key)
-        if ws is None:
-            ws = new_decode_workspace(S, p.n_head, p.n_kv_head, p.head_dim, start_pos + S,
-                                      self._window(layer), self.device)
-            self._batch_ws[key] = ws
-        out = attn_decode(qr.view(S, p.n_head, p.head_dim), self.key_cache[layer],
-                          self.val_cache[layer], self._lens[start_pos:start_pos + S],
-                          start_pos + S, p.n_kv_head, window=self._window(layer),
-                          scale=self.scale, seq_stride=0, workspace=ws)
-        return out.view(S, -1)
 
     def supports_batched_prefill(self) -> bool:
-        """Prefill runs on MFMA for every cache dtype at head_dim 64/128 (an
-        f32 cache with Q.K on bf16 hi + lo halves); an f32 cache at head_dim
-        256 takes the split-KV kernel with one ragged sequence per query row."""
+        """Prefill runs on MFMA for every cache dtype and head_dim (an f32
+        cache with Q.K on bf16 hi + lo halves)."""
         return True
 
     def _window(self, layer: int) -> int:
@@ -431,14 +412,6 @@ class GpuAttention:
         S = q.shape[0]
         if start_pos + S > p.n_ctx:
             raise L.UllmHipError(L.E_INVALID, "prompt exceeds the context")
-        if p.kv_dtype == torch.float32:
-            qr = self._append(layer, q, k, v, start_pos, torch.float32, (q_norm, k_norm),
-                              (q_bias, k_bias, v_bias))
-            if p.head_dim in (64, 128):  # f32 MFMA prefill (Q.K on bf16 hi + lo)
-                return attn_prefill(qr, self.key_cache[layer], self.val_cache[layer], p.n_head,
-                                    p.n_kv_head, p.head_dim, start_pos=start_pos,
-                                    window=self._window(layer), scale=self.scale)
-            return self._rows_decode(layer, qr, start_pos, S)
         qr = self._append(layer, q, k, v, start_pos, p.kv_dtype, (q_norm, k_norm),
                           (q_bias, k_bias, v_bias))
         return attn_prefill(qr, self.key_cache[layer], self.val_cache[layer], p.n_head,
@@ -491,8 +464,6 @@ class GpuAttention:
                              rotary_dim=self.rotary_dim, neox=p.rope_neox, q_norm=q_norm,
                              k_norm=k_norm, eps=p.eps, q_bias=q_bias, k_bias=k_bias,
                              v_bias=v_bias, q_dtype=q_dtype)
-        if p.kv_dtype == torch.float32 and p.head_dim not in (64, 128):
-            return self._rows_decode(layer, qr, start_pos, S)
         return attn_prefill(qr, self.key_cache[layer], self.val_cache[layer], p.n_head,
                             p.n_kv_head, p.head_dim, start_pos=start_pos,
                             window=self._window(layer), scale=self.scale)

@@ -1587,10 +1587,6 @@ extern "C" int ullm_hip_attn_prefill(const void *q, const void *k_cache, const v
                                      float scale, float *out, void *stream) {
     if (!dtype_ok(dtype))
         return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill: dtype %d", dtype);
-    if (dtype == ULLM_DT_F32 && head_dim == 256)
-        return set_error(ULLM_HIP_E_UNSUPPORTED,
-                         "prefill: an f32 cache takes head_dim 64 or 128 (256: attend row by row "
-                         "with ullm_hip_attn_decode)");
     if (n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || S < 0 || start_pos < 0)
         return set_error(ULLM_HIP_E_INVALID, "prefill: bad shape S=%d start_pos=%d heads=%d/%d", S,
                          start_pos, n_head, n_kv_head);
@@ -1612,6 +1608,9 @@ extern "C" int ullm_hip_attn_prefill(const void *q, const void *k_cache, const v
         // head_dim 128: prefill16_kernel's f32 mode (faster at every measured
         // prompt, 128..4096 rows); ULLM_HIP_PREFILL_F32=4 keeps prefill_f32_kernel.
         static const int ef = env_override("ULLM_HIP_PREFILL_F32");
+        if (head_dim == 256)
+            return launch_prefill16(ULLM_DT_F32, q, k_cache, v_cache, kv_stride, S, start_pos, window,
+                                    n_head, kv_mul, qs, out, st, KvPages{});
         if (head_dim == 128 && ef != 4)
             return launch_prefill16_128(ULLM_DT_F32, q, k_cache, v_cache, kv_stride, S, start_pos, window,
                                         n_head, kv_mul, qs, out, st, KvPages{});
@@ -1630,9 +1629,9 @@ extern "C" int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, c
                                            int table_len, int S, int start_pos, int window,
                                            int n_head, int n_kv_head, int head_dim, float scale,
                                            float *out, void *stream) {
-    if (dtype != ULLM_DT_F16 && dtype != ULLM_DT_BF16 && !(dtype == ULLM_DT_F32 && head_dim == 128))
-        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: dtype %d at head_dim %d (f16/bf16; f32 at 128)",
-                         dtype, head_dim);
+    if (dtype != ULLM_DT_F16 && dtype != ULLM_DT_BF16 && !(dtype == ULLM_DT_F32 && head_dim != 64))
+        return set_error(ULLM_HIP_E_UNSUPPORTED,
+                         "prefill_paged: dtype %d at head_dim %d (f16/bf16; f32 at 128 or 256)", dtype, head_dim);
     if (head_dim != 64 && head_dim != 128 && head_dim != 256)
         return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: head_dim %d not in {64,128,256}", head_dim);
     if (n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || S < 0 || start_pos < 0)
@@ -1660,9 +1659,13 @@ extern "C" int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, c
     const float qs = scale * kLog2e;
     const int kv_mul = n_head / n_kv_head;
     hipStream_t st = (hipStream_t)stream;
-    if (dtype == ULLM_DT_F32)  // f32 pages: prefill16_kernel's f32 mode
+    if (dtype == ULLM_DT_F32) {  // f32 pages: prefill16_kernel's f32 mode
+        if (head_dim == 256)
+            return launch_prefill16(ULLM_DT_F32, q, k_pages, v_pages, kv_stride, S, start_pos, window,
+                                    n_head, kv_mul, qs, out, st, pgs);
         return launch_prefill16_128(ULLM_DT_F32, q, k_pages, v_pages, kv_stride, S, start_pos, window,
                                     n_head, kv_mul, qs, out, st, pgs);
+    }
     if (dtype == ULLM_DT_BF16) {
         if (head_dim == 64) PrefillLaunch<BF16, 64>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);
         else if (head_dim == 128) PrefillLaunch<BF16, 128>::run(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head, kv_mul, qs, out, st, pgs);

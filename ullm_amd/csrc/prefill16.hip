@@ -67,7 +67,7 @@ __device__ __forceinline__ int p16_vswz(int r) { return ((r & 7) << 1) | ((r >> 
 // 160 KB holds (OCC workgroups per CU), at most 4.
 template <int KS, int DS, int D, int OCC, int EB = 2>
 constexpr int p16_stages() {
-    constexpr int stage = EB == 4 ? 2 * 32 * D * 4 : 32 * D * 2 + 32 * D * 2 / DS;
+    constexpr int stage = EB == 4 ? 32 * D * 4 + 32 * D * 4 / DS : 32 * D * 2 + 32 * D * 2 / DS;
     constexpr int st = 160 * 1024 / OCC / (KS * stage);
     return st > 4 ? 4 : st;
 }
@@ -90,10 +90,11 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
     using MT = typename std::conditional<F, BF16, T>::type;  // Q.K operand type
     constexpr int BN = 32, RB = D * 2, RBV = RB / DS;  // rows of the 16-bit tiles
     static_assert(D == 128 || D == 256, "head_dim");
-    static_assert(!F || (D == 128 && DS == 1), "f32 cache: head_dim 128, no value split");
+    static_assert(!F || KS == 1 || D == 128, "f32 cache at head_dim 256: one key stream");
     constexpr int RBF = D * T::bytes;  // cache bytes per key row of one head
+    constexpr int RBFV = RBF / DS;     // f32 V bytes fetched per key row
     constexpr int TILE = BN * RB, TILEV = BN * RBV;
-    constexpr int DMAK = F ? BN * RBF : TILE, DMAV = F ? BN * RBF : TILEV;  // bytes fetched
+    constexpr int DMAK = F ? BN * RBF : TILE, DMAV = F ? BN * RBFV : TILEV;  // bytes fetched
     constexpr int STAGE = DMAK + DMAV;
     constexpr int VOFF = F ? 2 * TILE : TILE;  // V tile in a stage (f32: after K hi, K lo)
     constexpr int NW = 8, NWS = NW / KS;  // waves per stream
@@ -167,8 +168,8 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
 #pragma unroll
     for (int i = 0; i < NICV; i++) {
         if constexpr (F) {
-            const int r = (ws * NICV + i) * (1024 / RBF) + lane / (RBF / 16);
-            vofs[i] = r * rbg + (lane % (RBF / 16)) * 16;
+            const int r = (ws * NICV + i) * (1024 / RBFV) + lane / (RBFV / 16);
+            vofs[i] = r * rbg + (lane % (RBFV / 16)) * 16 + dh * RBFV;
         } else {
             const int r = (ws * NICV + i) * (1024 / RBV) + lane / VSL;
             vofs[i] = r * rbg + ((((lane % VSL) ^ p16_vswz(r)) + dh * VSL) * 16);
@@ -217,7 +218,8 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
 #pragma unroll
             for (int i = 0; i < NICV; i++) {
                 tie(vx[i]);
-                const int r = (ws * NICV + i) * (1024 / RBF) + lane / FSL, sl = lane % FSL;
+                constexpr int FSLV = RBFV / 16;
+                const int r = (ws * NICV + i) * (1024 / RBFV) + lane / FSLV, sl = lane % FSLV;
                 const uint32_t o = base + VOFF + r * RBV + (((sl >> 1) ^ p16_vswz(r)) * 16) + (sl & 1) * 8;
                 lds_write_b64(o, u32x2{pack_f16x2(__uint_as_float(vx[i][0]), __uint_as_float(vx[i][1])),
                                        pack_f16x2(__uint_as_float(vx[i][2]), __uint_as_float(vx[i][3]))});
@@ -285,12 +287,12 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
         for (int i = 0; i < 4; i++) kaddr[i] = sb + ka[i];
 #pragma unroll
         for (int i = 0; i < 8; i++) vaddr[i] = sb + va[i];
-        u32x4 kb[2 * NKS], kl[F ? 2 * NKS : 1];
-        static_for<0, 2 * NKS>([&](auto ic) {
-            constexpr int idx = decltype(ic)::value, s = idx >> 1, kt = idx & 1;
-            kb[idx] = lds_read_b128_at<(s >> 2) * 256 + kt * 16 * RB>(kaddr[s & 3]);
-            if constexpr (F) kl[idx] = lds_read_b128_at<TILE + (s >> 2) * 256 + kt * 16 * RB>(kaddr[s & 3]);
-        });
+        u32x4 kb[F ? 1 : 2 * NKS];
+        if constexpr (!F)
+            static_for<0, 2 * NKS>([&](auto ic) {
+                constexpr int idx = decltype(ic)::value, s = idx >> 1, kt = idx & 1;
+                kb[idx] = lds_read_b128_at<(s >> 2) * 256 + kt * 16 * RB>(kaddr[s & 3]);
+            });
         u32x4 vb[NDT];
         auto rdv = [&](auto dtc) {
             constexpr int dt = decltype(dtc)::value;
@@ -299,16 +301,31 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
             vb[dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         };
         if constexpr (F) {
-            lds_wait_any();  // every K hi and lo read; then all V^T reads under the MFMAs
-            rdv(Int<0>{}); rdv(Int<1>{}); rdv(Int<2>{}); rdv(Int<3>{});
-            rdv(Int<4>{}); rdv(Int<5>{}); rdv(Int<6>{}); rdv(Int<7>{});
-            static_for<0, 2 * NKS>([&](auto ic) {
-                constexpr int idx = decltype(ic)::value, s = idx >> 1, kt = idx & 1;
-                tie(kb[idx]);
-                tie(kl[idx]);
-                sacc[kt] = mfma16<MT>(kb[idx], qreg[s], sacc[kt]);
-                sacc[kt] = mfma16<MT>(kb[idx], qlo[s], sacc[kt]);
-                sacc[kt] = mfma16<MT>(kl[idx], qreg[s], sacc[kt]);
+            // K hi and lo in batches of 8 operands each (head_dim 256: two
+            // batches); the V^T reads go out with the last batch's MFMAs.
+            static_assert(NDT == 8, "f32 mode: 8 value d tiles per workgroup");
+            constexpr int CH = 2 * NKS > 8 ? 8 : 2 * NKS;
+            static_for<0, 2 * NKS / CH>([&](auto hc) {
+                constexpr int h = decltype(hc)::value;
+                u32x4 kh[CH], kl[CH];
+                static_for<0, CH>([&](auto ic) {
+                    constexpr int idx = h * CH + decltype(ic)::value, s = idx >> 1, kt = idx & 1;
+                    kh[idx - h * CH] = lds_read_b128_at<(s >> 2) * 256 + kt * 16 * RB>(kaddr[s & 3]);
+                    kl[idx - h * CH] = lds_read_b128_at<TILE + (s >> 2) * 256 + kt * 16 * RB>(kaddr[s & 3]);
+                });
+                lds_wait_any();
+                if constexpr (h == 2 * NKS / CH - 1) {
+                    rdv(Int<0>{}); rdv(Int<1>{}); rdv(Int<2>{}); rdv(Int<3>{});
+                    rdv(Int<4>{}); rdv(Int<5>{}); rdv(Int<6>{}); rdv(Int<7>{});
+                }
+                static_for<0, CH>([&](auto ic) {
+                    constexpr int i = decltype(ic)::value, idx = h * CH + i, s = idx >> 1, kt = idx & 1;
+                    tie(kh[i]);
+                    tie(kl[i]);
+                    sacc[kt] = mfma16<MT>(kh[i], qreg[s], sacc[kt]);
+                    sacc[kt] = mfma16<MT>(kh[i], qlo[s], sacc[kt]);
+                    sacc[kt] = mfma16<MT>(kl[i], qreg[s], sacc[kt]);
+                });
             });
         } else {
         lds_wait_n<NKS>();  // the first half of the K reads
@@ -529,7 +546,13 @@ int launch_prefill16(int dtype, const void *q, const void *kc, const void *vc, i
             else go(prefill16_kernel<T, 1, 1>);
         }
     };
-    if (dtype == ULLM_DT_BF16) pick(BF16{});
+    if (dtype == ULLM_DT_F32) {  // f32 cache: one key stream, value columns split
+        const int hw1 = p16_hw(kv_mul, 8), UR1 = 16 * 8 / hw1;
+        const int nu1 = (S + UR1 - 1) / UR1, nhg1 = n_head / hw1;
+        hipLaunchKernelGGL((prefill16_kernel<F32, 1, 2>), dim3((unsigned)(nu1 * nhg1 * 2)), dim3(512), 0, st,
+                           (const uint16_t *)q, (const char *)kc, (const char *)vc, kvs, S, start_pos,
+                           window, n_head, kv_mul, hw1, nhg1, nu1, qs, out, pgs);
+    } else if (dtype == ULLM_DT_BF16) pick(BF16{});
     else pick(F16{});
     return check_hip(hipGetLastError(), "prefill (16-row waves) launch");
 }
