@@ -68,7 +68,9 @@ __device__ __forceinline__ int p16_vswz(int r) { return ((r & 7) << 1) | ((r >> 
 template <int KS, int DS, int D, int OCC, int EB = 2>
 constexpr int p16_stages() {
     constexpr int stage = EB == 4 ? 32 * D * 4 + 32 * D * 4 / DS : 32 * D * 2 + 32 * D * 2 / DS;
-    constexpr int st = 160 * 1024 / OCC / (KS * stage);
+    // f32, one key stream, head_dim 128: two converted tiles beside the ring
+    constexpr int conv = EB == 4 && KS == 1 && D == 128 ? 2 * (2 * 32 * D * 2 + 32 * D * 2 / DS) : 0;
+    constexpr int st = (160 * 1024 / OCC - conv) / (KS * stage);
     return st > 4 ? 4 : st;
 }
 
@@ -97,6 +99,12 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
     constexpr int DMAK = F ? BN * RBF : TILE, DMAV = F ? BN * RBFV : TILEV;  // bytes fetched
     constexpr int STAGE = DMAK + DMAV;
     constexpr int VOFF = F ? 2 * TILE : TILE;  // V tile in a stage (f32: after K hi, K lo)
+    // f32 with one key stream at head_dim 128: the converted tiles go to two
+    // buffers of their own beside the f32 ring (alternating steps), so the
+    // conversion needs no barrier of its own: a wave's DMA and its reads of
+    // the f32 ring touch only its own chunks.
+    constexpr bool SEP = F && KS == 1 && D == 128;
+    constexpr int CONV = VOFF + TILEV;  // converted K hi, K lo and V tiles
     constexpr int NW = 8, NWS = NW / KS;  // waves per stream
     constexpr int NIC = DMAK / 1024 / NWS;    // 1 KiB DMA chunks per wave, K
     constexpr int NICV = DMAV / 1024 / NWS;  // and V
@@ -105,12 +113,12 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
     constexpr float kLazy = 8.0f;
     static_assert(KS == 1 || KS == 2, "key streams");
     static_assert(DS == 1 || DS == 2, "value column split");
-    static_assert(NSTG >= 2 && KS * NSTG * STAGE <= 160 * 1024 / OCC, "LDS ring");
+    static_assert(NSTG >= 2 && KS * NSTG * STAGE + (SEP ? 2 * CONV : 0) <= 160 * 1024 / OCC, "LDS ring");
     static_assert(NIC >= 1 && NICV >= 1, "DMA chunks per wave");
     // The V swizzle permutes the 16 slots of each 256-byte half of a row: V
     // rows of at least 256 bytes (no value split at head_dim 128).
     static_assert(RBV >= 256, "V rows of 256 bytes or more");
-    __shared__ __attribute__((aligned(1024))) char lds[KS * NSTG * STAGE];
+    __shared__ __attribute__((aligned(1024))) char lds[KS * NSTG * STAGE + (SEP ? 2 * CONV : 0)];
 
     const int dh = DS == 1 ? 0 : (int)(blockIdx.x % DS);  // value half
     const int bx = (int)(blockIdx.x / DS);
@@ -193,9 +201,11 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
     // bf16 V -> f16 in place, for the chunks this wave's DMA wrote; f32 K and
     // V -> bf16 hi/lo K and f16 V tiles (every wave reads its f32 chunks,
     // a barrier, then the converted writes: they land on other waves' rows).
-    auto widen = [&](int stg) {
+    auto widen = [&](int j) {
+        const int stg = j % NSTG;
         if constexpr (F) {
             const uint32_t base = lds_addr(ring + stg * STAGE);
+            const uint32_t obase = SEP ? lds_addr(lds + NSTG * STAGE + (j & 1) * CONV) : base;
             u32x4 kx[NIC], vx[NICV];
 #pragma unroll
             for (int i = 0; i < NIC; i++) kx[i] = lds_read_b128(base + (ws * NIC + i) * 1024 + lane * 16);
@@ -203,7 +213,7 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
             for (int i = 0; i < NICV; i++)
                 vx[i] = lds_read_b128(base + DMAK + (ws * NICV + i) * 1024 + lane * 16);
             lds_wait_any();
-            asm volatile("s_barrier" ::: "memory");
+            if constexpr (!SEP) asm volatile("s_barrier" ::: "memory");
             constexpr int FSL = RBF / 16;  // f32 slots per row: four elements each
 #pragma unroll
             for (int i = 0; i < NIC; i++) {
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
                 const int r = (ws * NIC + i) * (1024 / RBF) + lane / FSL, sl = lane % FSL;
                 const u32x2 a = split2<BF16>(__uint_as_float(kx[i][0]), __uint_as_float(kx[i][1]));
                 const u32x2 b = split2<BF16>(__uint_as_float(kx[i][2]), __uint_as_float(kx[i][3]));
-                const uint32_t o = base + r * RB + (((sl >> 1) ^ p16_kswz(r)) * 16) + (sl & 1) * 8;
+                const uint32_t o = obase + r * RB + (((sl >> 1) ^ p16_kswz(r)) * 16) + (sl & 1) * 8;
                 lds_write_b64(o, u32x2{a[0], b[0]});
                 lds_write_b64(o + TILE, u32x2{a[1], b[1]});
             }
@@ -220,7 +230,7 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
                 tie(vx[i]);
                 constexpr int FSLV = RBFV / 16;
                 const int r = (ws * NICV + i) * (1024 / RBFV) + lane / FSLV, sl = lane % FSLV;
-                const uint32_t o = base + VOFF + r * RBV + (((sl >> 1) ^ p16_vswz(r)) * 16) + (sl & 1) * 8;
+                const uint32_t o = obase + VOFF + r * RBV + (((sl >> 1) ^ p16_vswz(r)) * 16) + (sl & 1) * 8;
                 lds_write_b64(o, u32x2{pack_f16x2(__uint_as_float(vx[i][0]), __uint_as_float(vx[i][1])),
                                        pack_f16x2(__uint_as_float(vx[i][2]), __uint_as_float(vx[i][3]))});
             }
@@ -270,7 +280,7 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
     const uint32_t ring0 = lds_addr(ring);
 
     auto compute = [&](int j) {
-        const uint32_t sb = ring0 + (j % NSTG) * STAGE;
+        const uint32_t sb = SEP ? lds_addr(lds + NSTG * STAGE + (j & 1) * CONV) : ring0 + (j % NSTG) * STAGE;
         // LDS operand reads in batches of eight, each batch issued as soon as
         // the one two ahead has been waited for, so the read queue stays
         // busy under the MFMAs and the softmax (reads retire in order; at
@@ -444,7 +454,7 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
             tie(qreg[s]);
             if constexpr (F) tie(qlo[s]);
         }
-        widen(j % NSTG);
+        widen(j);
         lds_wait_any();
         asm volatile("s_barrier" ::: "memory");
         issue(j + NSTG - 1);
