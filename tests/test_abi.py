@@ -83,6 +83,10 @@ def test_prefill_and_append_validation():
     assert b"null" in lib.ullm_hip_last_error()
     assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_F32, 512, 16, 0, 0, 8, 2, 96, 0.1,
                                      None, None) == L.E_UNSUPPORTED
+    # q of 32768 rows x 128 heads x 256 (4 GiB) over a 32 MB one-kv-head cache
+    assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_F32, 256, 32768, 0, 0, 128, 1, 256,
+                                     0.1, None, None) == L.E_INVALID
+    assert b"q exceeds 2 GiB" in lib.ullm_hip_last_error()
     assert lib.ullm_hip_attn_prefill(None, None, None, 7, 256, 16, 0, 0, 8, 2, 128, 0.1,
                                      None, None) == L.E_UNSUPPORTED
     assert lib.ullm_hip_attn_prefill(None, None, None, L.DT_BF16, 256, 16, 0, 0, 8, 3, 128,
@@ -202,6 +206,9 @@ def test_paged_prefill_validation():
     assert call(dt=L.DT_F32) == L.E_INVALID              # accepted; then the null pointers
     assert call(dt=L.DT_F16, kvs=1028) == L.E_INVALID    # 2056-byte rows: not
     assert call(d=96) == L.E_UNSUPPORTED
+    # q of 32768 rows x 128 heads x 256 f32 = 4 GiB over a 1-kv-head cache
+    assert call(dt=L.DT_F32, kvs=256, s=32768, tl=600, h=128, hk=1, d=256) == L.E_INVALID
+    assert b"q exceeds 2 GiB" in L.lib().ullm_hip_last_error()
     assert call(page=32) == L.E_INVALID   # below one 64-key tile
     assert call(page=96) == L.E_INVALID
     assert call(tl=7) == L.E_INVALID      # 7 pages < 512 positions

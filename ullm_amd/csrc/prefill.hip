@@ -1596,6 +1596,8 @@ extern "C" int ullm_hip_attn_prefill(const void *q, const void *k_cache, const v
         return set_error(ULLM_HIP_E_INVALID, "prefill: kv_stride must be >= n_kv_head*head_dim and 16-byte aligned");
     if ((int64_t)(start_pos + S) * kv_stride * dtype_bytes(dtype) > 0x7fff0000LL)
         return set_error(ULLM_HIP_E_INVALID, "prefill: a layer's cache exceeds 2 GiB");
+    if ((int64_t)S * n_head * head_dim * dtype_bytes(dtype) > 0x7fff0000LL)  // q's buffer range
+        return set_error(ULLM_HIP_E_INVALID, "prefill: q exceeds 2 GiB (split the prompt into chunks)");
     if (S == 0) return ULLM_HIP_OK;
     if (!q || !k_cache || !v_cache || !out)
         return set_error(ULLM_HIP_E_INVALID, "prefill: null tensor pointer");
@@ -1646,6 +1648,8 @@ extern "C" int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, c
                          page_size);
     if ((int64_t)page_size * kv_stride * eb > 0x7fff0000LL)
         return set_error(ULLM_HIP_E_INVALID, "prefill_paged: a page exceeds 2 GiB");
+    if ((int64_t)S * n_head * head_dim * eb > 0x7fff0000LL)  // q's buffer range
+        return set_error(ULLM_HIP_E_INVALID, "prefill_paged: q exceeds 2 GiB (split the prompt into chunks)");
     if (n_pages < 1) return set_error(ULLM_HIP_E_INVALID, "prefill_paged: n_pages %d < 1", n_pages);
     if ((int64_t)table_len * page_size < (int64_t)start_pos + S)
         return set_error(ULLM_HIP_E_INVALID, "prefill_paged: table of %d pages holds fewer than %d positions",
