@@ -40,10 +40,10 @@ def _decode_case(seed):
     return dict(H=H, Hk=Hk, D=D, dtype=dtype, lens=lens, window=window, pad=pad)
 
 
-def _prefill_case(seed):
-    rng = np.random.default_rng(2000 + seed)
+def _prefill_case(seed, dtypes=("f16", "bf16"), base=2000):
+    rng = np.random.default_rng(base + seed)
     H, Hk, D = _shape(rng)
-    dtype = str(rng.choice(["f16", "bf16"]))
+    dtype = str(rng.choice(list(dtypes)))
     S = int(rng.integers(1, 1500))
     start_pos = int(rng.choice([0, 0, 1, 77, 640]))
     window = int(rng.choice([0, 0, 0, 1, 100, 700]))
@@ -77,7 +77,17 @@ def test_decode_random(dev, seed):
 
 @pytest.mark.parametrize("seed", range(16))
 def test_prefill_random(dev, seed):
-    c = _prefill_case(seed)
+    check_prefill(dev, seed, _prefill_case(seed))
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_prefill_random_f32_cache(dev, seed):
+    """The reference's own f32 cache at every head_dim (64 on
+    prefill_f32_kernel, 128 and 256 on prefill16_kernel's f32 mode)."""
+    check_prefill(dev, seed, _prefill_case(seed, ("f32",), base=2500))
+
+
+def check_prefill(dev, seed, c):
     print(f"[prefill-rand] seed={seed} {c}", flush=True)
     H, Hk, D, S, sp = c["H"], c["Hk"], c["D"], c["S"], c["start_pos"]
     dt = DT[c["dtype"]]
