@@ -612,6 +612,7 @@ def main():
     if want("f32prefill"):
         # The reference's own cache dtype (f32) through the MFMA prefill.
         res["f32_prefill"] = bench_prefill(torch, A, args, 2048, 32, 8, 128, torch.float32)
+        res["f32_prefill_d256"] = bench_prefill(torch, A, args, 1024, 8, 4, 256, torch.float32)
     if want("cfg1"):
         res["cfg1"] = bench_decode(torch, A, args, 32, 8, 64, 512, 28, torch.float32, "cfg1")
     if want("cfg4"):
@@ -729,7 +730,16 @@ def main():
                         "tflops": round(res["f32_prefill"]["tflops"], 2),
                         "frac_mfma": round(res["f32_prefill"]["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
                         "note": "the matrix cores execute 2x the algorithmic FLOP (three bf16 "
-                                "products for Q.K)"},
+                                "products for Q.K)",
+                        "head_dim_256": {
+                            "workload": "cfg4 shape (S=1024, 8/4 heads, head_dim 256, causal) "
+                                        "over an f32 cache",
+                            "kernel": "prefill16_kernel<F32,1,2,256> (one key stream, value "
+                                      "columns split over two workgroups)",
+                            "ms": round(res["f32_prefill_d256"]["ms"], 4),
+                            "tflops": round(res["f32_prefill_d256"]["tflops"], 2),
+                            "frac_mfma": round(res["f32_prefill_d256"]["tflops"]
+                                               / MFMA_BF16_PEAK_TFLOPS, 4)}},
         "long_decode": {"workload": "cfg5 Qwen3-30B-A3B-shaped decode, 32/4 heads, head_dim "
                                     "128, bf16 KV 32768, 48 layers",
                         "us_per_layer": round(lc["us_per_layer"], 3),
