@@ -1,7 +1,7 @@
 // Causal prefill with 16-row waves, two per SIMD (gfx950): head_dim 256, and
 // head_dim 128 for short prompts (prefill.hip picks it where prefill4_kernel's
 // causal pairs would leave half the CUs idle).  Over an f32 cache (T = F32,
-// head_dim 128 and 256) it is the only prefill at those head dims: K and V
+// head_dim 128 and 256) it is the default prefill at those head dims: K and V
 // arrive as f32 tiles and are split in LDS into bf16 hi/lo K and f16 V tiles,
 // and Q.K runs as three bf16 products (Khi.Qhi + Khi.Qlo + Klo.Qhi).
 //
