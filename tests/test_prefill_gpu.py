@@ -314,3 +314,27 @@ def test_cfg3_pipeline_norm_rope_all_rows(dev):
         assert np.mean(got != want) < 0.01, f"append {name}: {np.mean(got != want):.3%} differ"
     ref2 = ora.attn_prefill(oq, okc, ovc, S, 0, H, Hk, D, scale)
     assert_close(out, ref2, what="cfg3 pipeline vs the oracle pipeline")
+
+
+@pytest.mark.parametrize("dtype,D", [("bf16", 128), ("f16", 256)])
+def test_q_past_the_call_limit_runs_in_chunks(dev, monkeypatch, dtype, D):
+    """attn_prefill splits a q at or above PREFILL_Q_MAX_BYTES into row chunks
+    at increasing start_pos (the limit is lowered here to 100 rows, so a
+    300-row prompt at start_pos 50 runs as 100 + 100 + 100 rows): every row
+    against the oracle, and against the one-call result within the
+    attention tolerance (the chunks run other workgroup plans)."""
+    S, sp, H, Hk = 300, 50, 8, 2
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16}[dtype]
+    q = synth.randn(31, 1, (S, H * D), dt).to(dev)
+    k = synth.randn(31, 2, (sp + S, Hk * D), dt).to(dev)
+    v = synth.randn(31, 3, (sp + S, Hk * D), dt).to(dev)
+    whole = A.attn_prefill(q, k, v, H, Hk, D, start_pos=sp, window=120)
+    monkeypatch.setattr(A, "PREFILL_Q_MAX_BYTES", 100 * H * D * q.element_size())
+    chunked = A.attn_prefill(q, k, v, H, Hk, D, start_pos=sp, window=120)
+    torch.cuda.synchronize()
+    rows = list(range(S))
+    ref = ora.attn_prefill(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                           v.float().cpu().numpy(), S, sp, H, Hk, D, 1.0 / math.sqrt(D),
+                           window=120, rows=rows)
+    assert_close(chunked.cpu().numpy(), ref, what="chunked")
+    assert_close(chunked.cpu().numpy(), whole.cpu().numpy(), what="chunked vs one call")

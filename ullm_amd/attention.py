@@ -182,13 +182,21 @@ def attn_prefill_paged(q, k_pages, v_pages, block_table, n_head, n_kv_head, head
     return out
 
 
+# Largest q the prefill entry points take in one call (below 2 GiB, and a
+# multiple of 16 bytes so every chunk stays 16-byte aligned).
+PREFILL_Q_MAX_BYTES = 0x7fff0000
+
+
 def attn_prefill(q, k_cache, v_cache, n_head, n_kv_head, head_dim, *, start_pos=0, window=0,
                  scale=None, kv_stride=None, out=None, stream=None):
     """Causal prefill attention on MFMA (lib.rs:1061-1087).
 
-    q: [S, n_head*head_dim] in the cache dtype (f16/bf16; or f32 with an f32
-    cache, head_dim 64/128); the cache already holds positions
-    0..start_pos+S-1.  Returns [S, n_head*head_dim] f32.
+    q: [S, n_head*head_dim] in the cache dtype (f16, bf16 or f32); the cache
+    already holds positions 0..start_pos+S-1.  Returns [S, n_head*head_dim]
+    f32.  A q of PREFILL_Q_MAX_BYTES or more (the kernels address it through
+    a 32-bit buffer range) runs as row chunks at increasing start_pos: the
+    cache already holds every position, so each chunk's rows see the same
+    keys.
     """
     S = q.shape[0]
     _need_cuda(q, k_cache, v_cache)
@@ -202,10 +210,15 @@ def attn_prefill(q, k_cache, v_cache, n_head, n_kv_head, head_dim, *, start_pos=
         scale = 1.0 / math.sqrt(head_dim)
     if out is None:
         out = torch.empty(S, n_head * head_dim, dtype=torch.float32, device=q.device)
-    rc = L.lib().ullm_hip_attn_prefill(
-        _ptr(q), _ptr(k_cache), _ptr(v_cache), _dt(q), kv_stride, S, start_pos, window, n_head,
-        n_kv_head, head_dim, float(scale), _ptr(out), _stream(stream))
-    L.check(rc)
+    row_bytes = n_head * head_dim * q.element_size()
+    rows = max(1, PREFILL_Q_MAX_BYTES // row_bytes)
+    for r0 in range(0, max(S, 1), rows):
+        n = min(rows, S - r0)
+        rc = L.lib().ullm_hip_attn_prefill(
+            _ptr(q[r0:r0 + n]), _ptr(k_cache), _ptr(v_cache), _dt(q), kv_stride, n,
+            start_pos + r0, window, n_head, n_kv_head, head_dim, float(scale),
+            _ptr(out[r0:r0 + n]), _stream(stream))
+        L.check(rc)
     return out
 
 
