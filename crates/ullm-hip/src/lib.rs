@@ -6,12 +6,22 @@
 //! `[n_layer][n_ctx][n_kv_head * head_dim]` (forward.rs:355-356), the RoPE
 //! table and the workspaces -- and keeps its surface: `new`, per-token
 //! `forward` (forward.rs:384, attention part :415-466), batched
-//! `forward_batch` (forward.rs:757, attention part :799-858) and
-//! `supports_batched_prefill` (forward.rs:744).  Like `GpuForward` it is
-//! `Send` but not `Sync`: one caller at a time (forward.rs:221-225).
+//! `forward_batch` (forward.rs:757, attention part :799-858),
+//! `supports_batched_prefill` (forward.rs:744) and `forward_debug`
+//! (forward.rs:530-635).  Like `GpuForward` it is `Send` but not `Sync`: one
+//! caller at a time (forward.rs:221-225).
 //!
-//! Not compiled here: the build image of this repository has no cargo.
-//! Every call it makes is one the repository's tests drive through ctypes.
+//! Device-resident path: `forward_dev` / `forward_batch_dev` take device
+//! views (`DevSlice`) of the f32 projections and the output, queue the fused
+//! append and the attention on one stream, and neither copy nor wait, so a
+//! whole token's layers run back to back and the caller synchronises once
+//! (`synchronize`), as GpuForward commits one command buffer and waits once
+//! (forward.rs:406-509).  `forward` / `forward_batch` are host-slice
+//! conveniences over them (upload, run, read back).
+//!
+//! Unverified: the build image of this repository has no cargo, so this
+//! crate has never been compiled or run.  Every C entry point it calls is
+//! one the repository's tests drive through ctypes.
 use std::os::raw::{c_int, c_void};
 
 use ullm_core::{Error, Result};
@@ -26,6 +36,7 @@ mod hip {
         pub fn hipFree(p: *mut c_void) -> c_int;
         pub fn hipMemset(p: *mut c_void, v: c_int, bytes: usize) -> c_int;
         pub fn hipMemcpy(dst: *mut c_void, src: *const c_void, bytes: usize, kind: c_int) -> c_int;
+        pub fn hipStreamSynchronize(stream: *mut c_void) -> c_int;
     }
     pub const H2D: c_int = 1;
     pub const D2H: c_int = 2;
@@ -35,6 +46,37 @@ mod hip {
 pub struct DevBuf {
     ptr: *mut c_void,
     bytes: usize,
+}
+
+/// A borrowed byte range of device memory: what the `*_dev` calls take for
+/// their inputs and outputs, so a step's tensors stay on the device
+/// (GpuForward keeps q, the K/V rows and the attention output in its own
+/// Metal buffers, forward.rs:384-515).
+#[derive(Clone, Copy, Debug)]
+pub struct DevSlice {
+    ptr: *mut c_void,
+    bytes: usize,
+}
+
+impl DevSlice {
+    /// A view of raw device memory the caller owns (e.g. its projection
+    /// outputs).  Safety: `ptr` must address `bytes` of device memory that
+    /// outlives every call given this view.
+    pub unsafe fn from_raw(ptr: *mut c_void, bytes: usize) -> Self {
+        Self { ptr, bytes }
+    }
+    pub fn ptr(&self) -> *mut c_void {
+        self.ptr
+    }
+    pub fn bytes(&self) -> usize {
+        self.bytes
+    }
+    fn need_f32(&self, n: usize, what: &str) -> Result<*mut f32> {
+        if self.bytes < n * 4 {
+            return Err(Error::Format(format!("{what}: {} bytes for {n} f32", self.bytes)));
+        }
+        Ok(self.ptr.cast())
+    }
 }
 
 impl DevBuf {
@@ -64,15 +106,19 @@ impl DevBuf {
         let rc = unsafe { hip::hipMemcpy(self.at(off), src.as_ptr().cast(), n, hip::H2D) };
         (rc == 0).then_some(()).ok_or_else(|| Error::Format("hipMemcpy H2D failed".into()))
     }
-    /// Copy to host from the start of the buffer (synchronous: this is the
-    /// one synchronisation point of a step, as commit + wait is in Metal).
-    pub fn download(&self, dst: &mut [f32]) -> Result<()> {
+    /// Copy `dst.len()` elements from byte offset `off` to host
+    /// (synchronous: it waits for the work queued before it, as commit +
+    /// wait does in Metal).
+    pub fn download_at<T: Copy>(&self, dst: &mut [T], off: usize) -> Result<()> {
         let n = std::mem::size_of_val(dst);
-        if n > self.bytes {
-            return Err(Error::Format(format!("download of {n} bytes past {}", self.bytes)));
+        if off + n > self.bytes {
+            return Err(Error::Format(format!("download of {n} bytes at {off} past {}", self.bytes)));
         }
-        let rc = unsafe { hip::hipMemcpy(dst.as_mut_ptr().cast(), self.ptr, n, hip::D2H) };
+        let rc = unsafe { hip::hipMemcpy(dst.as_mut_ptr().cast(), self.at(off), n, hip::D2H) };
         (rc == 0).then_some(()).ok_or_else(|| Error::Format("hipMemcpy D2H failed".into()))
+    }
+    pub fn download(&self, dst: &mut [f32]) -> Result<()> {
+        self.download_at(dst, 0)
     }
     pub fn ptr(&self) -> *mut c_void {
         self.ptr
@@ -80,12 +126,58 @@ impl DevBuf {
     pub fn at(&self, byte_off: usize) -> *mut c_void {
         unsafe { self.ptr.cast::<u8>().add(byte_off).cast() }
     }
+    /// The whole buffer as a device view.
+    pub fn view(&self) -> DevSlice {
+        DevSlice { ptr: self.ptr, bytes: self.bytes }
+    }
+    /// `bytes` from byte offset `off` as a device view.
+    pub fn slice(&self, off: usize, bytes: usize) -> Result<DevSlice> {
+        if off + bytes > self.bytes {
+            return Err(Error::Format(format!("view of {bytes} bytes at {off} past {}", self.bytes)));
+        }
+        Ok(DevSlice { ptr: self.at(off), bytes })
+    }
 }
 
 impl Drop for DevBuf {
     fn drop(&mut self) {
         unsafe { hip::hipFree(self.ptr) };
     }
+}
+
+/// NaN count, inf count and largest finite |value|: one line of
+/// `forward_debug`'s report (forward.rs:558-569).
+#[derive(Debug, Clone)]
+pub struct DebugStat {
+    pub label: &'static str,
+    pub nan: usize,
+    pub inf: usize,
+    pub maxabs: f32,
+}
+
+fn stat(label: &'static str, v: &[f32]) -> DebugStat {
+    let nan = v.iter().filter(|x| x.is_nan()).count();
+    let inf = v.iter().filter(|x| x.is_infinite()).count();
+    let maxabs = v.iter().copied().filter(|x| x.is_finite()).fold(0f32, |a, b| a.max(b.abs()));
+    DebugStat { label, nan, inf, maxabs }
+}
+
+/// 16-bit cache element -> f32 (the cache dtype's own bits).
+fn half_to_f32(h: u16, dtype: c_int) -> f32 {
+    if dtype == ffi::ULLM_DT_BF16 {
+        return f32::from_bits((h as u32) << 16);
+    }
+    let neg = h >> 15 != 0;
+    let exp = ((h >> 10) & 0x1f) as i32;
+    let man = (h & 0x3ff) as u32;
+    let mag = if exp == 0x1f {
+        f32::from_bits(0x7f80_0000 | (man << 13))
+    } else if exp == 0 {
+        man as f32 * (2f32).powi(-24) // zero or subnormal
+    } else {
+        f32::from_bits((((exp - 15 + 127) as u32) << 23) | (man << 13))
+    };
+    if neg { -mag } else { mag }
 }
 
 /// The attention fields of GpuParams (forward.rs:23-51), plus the cache
@@ -136,9 +228,16 @@ pub struct HipAttention {
     lens: DevBuf,
     ws: DevBuf,
     ws_bytes: usize,
-    q: DevBuf,
-    kv: DevBuf,
-    out: DevBuf,
+    /// Prepared q (bias, norm, RoPE applied) in the dtype the attention
+    /// reads: f32 for the decode and the f32-cache prefill, the cache dtype
+    /// for a 16-bit prefill.  [n_ctx][n_head*D] f32 bytes.
+    qprep: DevBuf,
+    /// Staging for the host-slice wrappers only: q, k and v rows uploaded
+    /// before the device path runs, and the output read back after it.
+    host_in: DevBuf,
+    host_out: DevBuf,
+    /// The HIP stream every launch goes to (null: the default stream).
+    stream: *mut c_void,
 }
 
 unsafe impl Send for HipAttention {}
@@ -173,14 +272,29 @@ impl HipAttention {
             lens: DevBuf::from_slice(&lens)?,
             ws: DevBuf::zeroed(ws_bytes)?,
             ws_bytes,
-            q: DevBuf::zeroed(p.n_ctx * q_dim * 4)?,
-            kv: DevBuf::zeroed(2 * p.n_ctx * kv_dim * 4)?,
-            out: DevBuf::zeroed(p.n_ctx * q_dim * 4)?,
+            qprep: DevBuf::zeroed(p.n_ctx * q_dim * 4)?,
+            host_in: DevBuf::zeroed(p.n_ctx * (q_dim + 2 * kv_dim) * 4)?,
+            host_out: DevBuf::zeroed(p.n_ctx * q_dim * 4)?,
+            stream: std::ptr::null_mut(),
         })
     }
 
     pub fn supports_batched_prefill(&self) -> bool {
         true
+    }
+
+    /// Launch on `stream` (a hipStream_t; null = the default stream) from
+    /// now on.  Safety: the stream must outlive this object's use of it.
+    pub unsafe fn set_stream(&mut self, stream: *mut c_void) {
+        self.stream = stream;
+    }
+
+    /// Wait for everything queued on this object's stream: the one
+    /// synchronisation of a token, as commit + wait_until_completed ends
+    /// GpuForward::forward (forward.rs:507-509).
+    pub fn synchronize(&self) -> Result<()> {
+        let rc = unsafe { hip::hipStreamSynchronize(self.stream) };
+        (rc == 0).then_some(()).ok_or_else(|| Error::Format("hipStreamSynchronize failed".into()))
     }
 
     /// Gemma-style local layers (forward.rs:450-454): every layer but each
@@ -198,90 +312,198 @@ impl HipAttention {
     fn scale(&self) -> f32 {
         (self.p.head_dim as f32).sqrt().recip() // forward.rs:399
     }
+    fn q_dim(&self) -> usize {
+        self.p.n_head * self.p.head_dim
+    }
+    fn check_layer(&self, layer: usize) -> Result<()> {
+        if layer >= self.p.n_layer {
+            return Err(Error::Format(format!("layer {layer} >= n_layer {}", self.p.n_layer)));
+        }
+        Ok(())
+    }
 
     /// Bias, Q/K norm, RoPE and the cache store of `rows` token rows at
-    /// positions start.. (lib.rs:1021-1058): f32 q/k/v in the `q`/`kv`
-    /// scratch, q out in `q_dtype` into `q_out`.
-    fn append(&self, layer: usize, rows: usize, start: usize, hp: HeadParams,
-              q_out: *mut c_void, q_dtype: c_int) -> Result<()> {
+    /// positions start.. (lib.rs:1021-1058): f32 q/k/v rows on the device,
+    /// q out in `q_dtype` into `q_out`.  Queued, not waited for.
+    #[allow(clippy::too_many_arguments)]
+    fn append(&self, layer: usize, rows: usize, start: usize, hp: HeadParams, q: *const f32,
+              k: *const f32, v: *const f32, q_out: *mut c_void, q_dtype: c_int) -> Result<()> {
         let (p, kd) = (&self.p, self.kv_dim);
         let off = self.layer_off(layer);
         ffi::check(unsafe {
             ffi::ullm_hip_qkv_append(
-                self.q.ptr.cast(), self.kv.ptr.cast(), self.kv.at(rows * kd * 4).cast(),
-                dev_f32(hp.q_bias), dev_f32(hp.k_bias), dev_f32(hp.v_bias),
+                q, k, v, dev_f32(hp.q_bias), dev_f32(hp.k_bias), dev_f32(hp.v_bias),
                 dev_f32(hp.q_norm), dev_f32(hp.k_norm), p.eps, self.rope_cs.ptr.cast(),
                 p.n_ctx as c_int, p.rope_neox as c_int, self.rd as c_int, rows as c_int,
                 start as c_int, p.n_head as c_int, p.n_kv_head as c_int, p.head_dim as c_int,
                 q_out, q_dtype, self.key_cache.at(off), self.val_cache.at(off), p.kv_dtype,
-                kd as i64, std::ptr::null_mut())
+                kd as i64, self.stream)
         })
     }
 
-    /// Decode one token at `pos` from its f32 projections q [n_head*D] and
-    /// k/v [kv_dim] (before bias, norm and RoPE): append, then attend
-    /// (forward.rs:415-466; lib.rs:857-938).  Returns [n_head*D] f32.
-    pub fn forward(&self, layer: usize, q: &[f32], k: &[f32], v: &[f32], pos: usize,
-                   hp: HeadParams) -> Result<Vec<f32>> {
+    /// The decode attention of layer `layer` at `pos` over the prepared q in
+    /// `qprep`, into `out`.  Queued, not waited for.
+    fn decode(&self, layer: usize, pos: usize, out: *mut f32) -> Result<()> {
         let (p, kd) = (&self.p, self.kv_dim);
-        if pos >= p.n_ctx {
-            return Err(Error::Format(format!("pos {pos} >= n_ctx {}", p.n_ctx)));
-        }
-        self.q.upload(q, 0)?;
-        self.kv.upload(k, 0)?;
-        self.kv.upload(v, kd * 4)?;
-        self.append(layer, 1, pos, hp, self.q.ptr, ffi::ULLM_DT_F32)?;
         let off = self.layer_off(layer);
         ffi::check(unsafe {
             ffi::ullm_hip_attn_decode(
-                self.q.ptr.cast(), self.key_cache.at(off), self.val_cache.at(off), p.kv_dtype,
-                kd as i64, 0, self.lens.at(pos * 4).cast(), (pos + 1) as c_int,
+                self.qprep.ptr.cast(), self.key_cache.at(off), self.val_cache.at(off),
+                p.kv_dtype, kd as i64, 0, self.lens.at(pos * 4).cast(), (pos + 1) as c_int,
                 self.window(layer), 1, p.n_head as c_int, p.n_kv_head as c_int,
-                p.head_dim as c_int, self.scale(), self.out.ptr.cast(), self.ws.ptr,
-                self.ws_bytes, std::ptr::null_mut())
-        })?;
-        let mut o = vec![0f32; p.n_head * p.head_dim];
-        self.out.download(&mut o)?;
-        Ok(o)
+                p.head_dim as c_int, self.scale(), out, self.ws.ptr, self.ws_bytes, self.stream)
+        })
     }
 
-    /// Prefill s tokens at positions 0..s from their f32 projections qs
-    /// [s][n_head*D] and ks/vs [s][kv_dim] (forward.rs:799-858;
-    /// lib.rs:1021-1087).  Returns [s][n_head*D] f32.
-    ///  * f16/bf16 cache: q goes out in the cache dtype, then one causal
+    /// Decode one token at `pos` with every tensor on the device: q
+    /// [n_head*D] and k/v [kv_dim] f32 projections (before bias, norm and
+    /// RoPE) in, [n_head*D] f32 attention output out.  Appends the K/V row to
+    /// layer `layer`'s cache, then attends (forward.rs:415-466;
+    /// lib.rs:857-938).  Two launches are queued on the stream and nothing
+    /// is copied or waited for: the caller runs its other layers and calls
+    /// `synchronize` once per token.
+    pub fn forward_dev(&self, layer: usize, q: DevSlice, k: DevSlice, v: DevSlice, pos: usize,
+                       hp: HeadParams, out: DevSlice) -> Result<()> {
+        let (p, kd, qd) = (&self.p, self.kv_dim, self.q_dim());
+        self.check_layer(layer)?;
+        if pos >= p.n_ctx {
+            return Err(Error::Format(format!("pos {pos} >= n_ctx {}", p.n_ctx)));
+        }
+        let (qp, kp, vp) = (q.need_f32(qd, "q")?, k.need_f32(kd, "k")?, v.need_f32(kd, "v")?);
+        let op = out.need_f32(qd, "out")?;
+        self.append(layer, 1, pos, hp, qp, kp, vp, self.qprep.ptr, ffi::ULLM_DT_F32)?;
+        self.decode(layer, pos, op)
+    }
+
+    /// Prefill s tokens at positions 0..s with every tensor on the device:
+    /// qs [s][n_head*D] and ks/vs [s][kv_dim] f32 projections in, [s][n_head*D]
+    /// f32 out (forward.rs:799-858; lib.rs:1021-1087).  Queued, not waited for.
+    ///  * f16/bf16 cache: q is prepared in the cache dtype, then one causal
     ///    prefill launch on the matrix cores.
     ///  * f32 cache (the reference's own): q stays f32 and the prefill
     ///    kernel runs Q.K on bf16 hi + lo halves.
-    pub fn forward_batch(&self, layer: usize, qs: &[f32], ks: &[f32], vs: &[f32], s: usize,
-                         hp: HeadParams) -> Result<Vec<f32>> {
-        let (p, kd) = (&self.p, self.kv_dim);
+    #[allow(clippy::too_many_arguments)]
+    pub fn forward_batch_dev(&self, layer: usize, qs: DevSlice, ks: DevSlice, vs: DevSlice,
+                             s: usize, hp: HeadParams, out: DevSlice) -> Result<()> {
+        let (p, kd, qd) = (&self.p, self.kv_dim, self.q_dim());
+        self.check_layer(layer)?;
         if s == 0 || s > p.n_ctx {
             return Err(Error::Format(format!("prompt of {s} tokens for n_ctx {}", p.n_ctx)));
         }
-        self.q.upload(qs, 0)?;
-        self.kv.upload(ks, 0)?;
-        self.kv.upload(vs, s * kd * 4)?;
+        let qp = qs.need_f32(s * qd, "qs")?;
+        let (kp, vp) = (ks.need_f32(s * kd, "ks")?, vs.need_f32(s * kd, "vs")?);
+        let op = out.need_f32(s * qd, "out")?;
+        self.append(layer, s, 0, hp, qp, kp, vp, self.qprep.ptr, p.kv_dtype)?;
         let off = self.layer_off(layer);
-        // 16-bit caches: q in the cache dtype goes to `out` and the
-        // attention writes its f32 rows to `q`.  An f32 cache: q is prepared
-        // in place in `q` and the attention writes `out`.
-        let q_prep = if p.kv_dtype == ffi::ULLM_DT_F32 { self.q.ptr } else { self.out.ptr };
-        let o_dst = if p.kv_dtype == ffi::ULLM_DT_F32 { self.out.ptr } else { self.q.ptr };
-        self.append(layer, s, 0, hp, q_prep, p.kv_dtype)?;
         ffi::check(unsafe {
             ffi::ullm_hip_attn_prefill(
-                q_prep, self.key_cache.at(off), self.val_cache.at(off), p.kv_dtype,
+                self.qprep.ptr, self.key_cache.at(off), self.val_cache.at(off), p.kv_dtype,
                 kd as i64, s as c_int, 0, self.window(layer), p.n_head as c_int,
-                p.n_kv_head as c_int, p.head_dim as c_int, self.scale(), o_dst.cast(),
-                std::ptr::null_mut())
-        })?;
-        if p.kv_dtype != ffi::ULLM_DT_F32 {
-            let mut o = vec![0f32; s * p.n_head * p.head_dim];
-            self.q.download(&mut o)?;
-            return Ok(o);
+                p.n_kv_head as c_int, p.head_dim as c_int, self.scale(), op, self.stream)
+        })
+    }
+
+    /// Host-slice form of `forward_dev` for callers whose projections live in
+    /// host memory: checks the slice lengths, uploads them, runs the device
+    /// path and reads the output back (the read is the step's one wait).
+    pub fn forward(&self, layer: usize, q: &[f32], k: &[f32], v: &[f32], pos: usize,
+                   hp: HeadParams) -> Result<Vec<f32>> {
+        let (kd, qd) = (self.kv_dim, self.q_dim());
+        if q.len() != qd || k.len() != kd || v.len() != kd {
+            return Err(Error::Format(format!(
+                "q/k/v of {}/{}/{} floats, expected {qd}/{kd}/{kd}", q.len(), k.len(), v.len())));
         }
-        let mut o = vec![0f32; s * p.n_head * p.head_dim];
-        self.out.download(&mut o)?;
+        let (qv, kv, vv) = self.stage(q, k, v, 1)?;
+        self.forward_dev(layer, qv, kv, vv, pos, hp, self.host_out.view())?;
+        let mut o = vec![0f32; qd];
+        self.host_out.download(&mut o)?;
         Ok(o)
+    }
+
+    /// Host-slice form of `forward_batch_dev` (lengths checked against s).
+    pub fn forward_batch(&self, layer: usize, qs: &[f32], ks: &[f32], vs: &[f32], s: usize,
+                         hp: HeadParams) -> Result<Vec<f32>> {
+        let (p, kd, qd) = (&self.p, self.kv_dim, self.q_dim());
+        if s == 0 || s > p.n_ctx {
+            return Err(Error::Format(format!("prompt of {s} tokens for n_ctx {}", p.n_ctx)));
+        }
+        if qs.len() != s * qd || ks.len() != s * kd || vs.len() != s * kd {
+            return Err(Error::Format(format!(
+                "qs/ks/vs of {}/{}/{} floats, expected {}/{}/{} for {s} tokens",
+                qs.len(), ks.len(), vs.len(), s * qd, s * kd, s * kd)));
+        }
+        let (qv, kv, vv) = self.stage(qs, ks, vs, s)?;
+        self.forward_batch_dev(layer, qv, kv, vv, s, hp, self.host_out.view())?;
+        let mut o = vec![0f32; s * qd];
+        self.host_out.download(&mut o)?;
+        Ok(o)
+    }
+
+    /// Upload host q/k/v rows into `host_in` and return device views of them.
+    fn stage(&self, q: &[f32], k: &[f32], v: &[f32], rows: usize)
+             -> Result<(DevSlice, DevSlice, DevSlice)> {
+        let (kd, qd) = (self.kv_dim, self.q_dim());
+        let (qb, kb) = (rows * qd * 4, rows * kd * 4);
+        self.host_in.upload(q, 0)?;
+        self.host_in.upload(k, qb)?;
+        self.host_in.upload(v, qb + kb)?;
+        Ok((self.host_in.slice(0, qb)?, self.host_in.slice(qb, kb)?,
+            self.host_in.slice(qb + kb, kb)?))
+    }
+
+    /// The attention half of GpuForward::forward_debug (forward.rs:530-635):
+    /// one decode step of layer `layer` at `pos`, one op at a time with a
+    /// wait after each, reporting NaN count, inf count and largest finite
+    /// |value| of every intermediate, printed as the reference prints them
+    /// (`[dbg posP] label nan=.. inf=.. maxabs=..`): the raw projections,
+    /// then q and the cache's K and V rows after the fused append (bias,
+    /// norm, RoPE, store), then the attention output.  The fused decode
+    /// never materialises the scores, so the report goes from rope_k to
+    /// attn_out.  Unlike the device path it synchronises after every op.
+    pub fn forward_debug(&self, layer: usize, q: &[f32], k: &[f32], v: &[f32], pos: usize,
+                         hp: HeadParams) -> Result<Vec<DebugStat>> {
+        let (p, kd, qd) = (&self.p, self.kv_dim, self.q_dim());
+        self.check_layer(layer)?;
+        if pos >= p.n_ctx {
+            return Err(Error::Format(format!("pos {pos} >= n_ctx {}", p.n_ctx)));
+        }
+        if q.len() != qd || k.len() != kd || v.len() != kd {
+            return Err(Error::Format(format!(
+                "q/k/v of {}/{}/{} floats, expected {qd}/{kd}/{kd}", q.len(), k.len(), v.len())));
+        }
+        let mut rep = Vec::new();
+        let mut log = |st: DebugStat| {
+            eprintln!("[dbg pos{pos}] {:<14} nan={} inf={} maxabs={:.4}", st.label, st.nan,
+                      st.inf, st.maxabs);
+            rep.push(st);
+        };
+        log(stat("wq", q));
+        log(stat("wk", k));
+        log(stat("wv", v));
+        let (qv, kv, vv) = self.stage(q, k, v, 1)?;
+        self.append(layer, 1, pos, hp, qv.ptr.cast(), kv.ptr.cast(), vv.ptr.cast(),
+                    self.qprep.ptr, ffi::ULLM_DT_F32)?;
+        self.synchronize()?;
+        let mut buf = vec![0f32; qd];
+        self.qprep.download(&mut buf)?;
+        log(stat("rope_q", &buf));
+        let row = self.layer_off(layer) + pos * kd * self.elt;
+        for (cache, label) in [(&self.key_cache, "rope_k"), (&self.val_cache, "v_row")] {
+            let vals = if p.kv_dtype == ffi::ULLM_DT_F32 {
+                let mut r = vec![0f32; kd];
+                cache.download_at(&mut r, row)?;
+                r
+            } else {
+                let mut r = vec![0u16; kd];
+                cache.download_at(&mut r, row)?;
+                r.iter().map(|&h| half_to_f32(h, p.kv_dtype)).collect()
+            };
+            log(stat(label, &vals));
+        }
+        self.decode(layer, pos, self.host_out.ptr.cast())?;
+        self.synchronize()?;
+        self.host_out.download(&mut buf)?;
+        log(stat("attn_out", &buf));
+        Ok(rep)
     }
 }

@@ -53,7 +53,9 @@ def test_cfg3_qwen3_4b_bf16_2048(dev):
 
 
 def test_cfg4_gemma3_f16_1024_window(dev):
-    run_case(dev, "f16", 1024, 8, 4, 256, window=1024, seed=4)
+    """cfg4's prefill at its full size, every one of the 1024 rows and 8
+    heads against the oracle."""
+    run_case(dev, "f16", 1024, 8, 4, 256, window=1024, seed=4, rows=list(range(1024)))
 
 
 @pytest.mark.parametrize("S,window", [(1536, 512), (700, 100), (300, 1)])

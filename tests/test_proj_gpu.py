@@ -115,7 +115,8 @@ def test_split_exchange_2000_calls_repeat_exactly(dev):
     back-to-back calls at the Qwen3-4B decode shape on one workspace, each
     call's q (written to its own row) and the final K/V row bit-identical to
     the first call's; a stale part reloaded by the last arriver would change
-    a head.  Stops at the first mismatching call."""
+    a head.  All calls are queued first; the comparison afterwards reports
+    the first mismatching call."""
     H, Hk, D, hidden, n = 32, 8, 128, 2560, 2000
     print(f"[proj] exchange repeat x{n}", flush=True)
     x = synth.randn(21, 1, (1, hidden)).to(dev)

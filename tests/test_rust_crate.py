@@ -48,3 +48,32 @@ def test_constants_match_the_header():
         cv = int(re.search(rf"\b{name}\s*=\s*(-?\d+)", h).group(1))
         rv = int(re.search(rf"pub const {name}: c_int = (-?\d+);", rs).group(1))
         assert cv == rv, name
+
+
+def _fn_body(src, name):
+    i = src.index(f"pub fn {name}(")
+    j = src.index("{", src.index(")", i))
+    depth, k = 0, j
+    while True:
+        depth += {"{": 1, "}": -1}.get(src[k], 0)
+        k += 1
+        if depth == 0:
+            return src[j:k]
+
+
+def test_device_path_neither_copies_nor_waits():
+    """forward_dev / forward_batch_dev queue launches only: no host copy and
+    no synchronisation inside them (the caller waits once per token), and
+    the surface GpuForward has (forward_debug included) is there."""
+    src = _strip_comments(open(os.path.join(ROOT, "crates", "ullm-hip", "src", "lib.rs")).read())
+    for name in ("forward_dev", "forward_batch_dev"):
+        body = _fn_body(src, name)
+        for banned in ("hipMemcpy", "upload", "download", "synchronize", "stage("):
+            assert banned not in body, f"{name} calls {banned}"
+    for name in ("new", "forward", "forward_batch", "supports_batched_prefill", "forward_debug",
+                 "synchronize"):
+        assert f"pub fn {name}(" in src, name
+    # the host-slice wrappers check the slice lengths before any upload
+    for name in ("forward", "forward_batch", "forward_debug"):
+        body = _fn_body(src, name)
+        assert "q.len()" in body or "qs.len()" in body, name
