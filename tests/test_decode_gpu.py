@@ -91,6 +91,25 @@ def test_block_splits(dev, dtype, H, Hk, D, L, window):
     run_case(dev, dtype, H, Hk, D, [L], window=window, seed=13)
 
 
+# The reference's f32 cache past the one- and two-block splits: long
+# contexts stream through decode_dma_kernel's f32 mode (f32 tiles by LDS DMA,
+# bf16 hi + lo products), one split per unit when the units fill the chip
+# (4-wave workgroups at head_dim 64, 2-wave at 128), windows and ragged
+# batches.
+@pytest.mark.parametrize("H,Hk,D,lens,window", [
+    (32, 4, 128, [32768], 0),                       # cfg5's shape with an f32 cache
+    (12, 2, 128, [20000], 0),
+    (32, 8, 64, [16384], 0),
+    (8, 4, 128, [5000], 333),
+    (16, 4, 64, [9000], 4096),
+    (32, 4, 128, [30000, 4100, 17000, 9000], 0),    # ragged batch, 2-wave workgroups
+    (16, 8, 128, [400] * 32, 0),                    # units fill the chip: one split per unit
+    (32, 8, 64, [300] * 64, 0),
+])
+def test_f32_cache_long(dev, H, Hk, D, lens, window):
+    run_case(dev, "f32", H, Hk, D, lens, window=window, seed=14, device_rng=True)
+
+
 def test_cfg5_qwen3_30b_bf16_32k(dev):
     run_case(dev, "bf16", 32, 4, 128, [32768], seed=5, device_rng=True)
 

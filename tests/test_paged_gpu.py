@@ -75,8 +75,12 @@ CASES = [
     ([5000, 4100, 40], 8, 4, 64, "bf16", 32, 37, 0),
     ([33000, 12000], 32, 4, 128, "bf16", 512, 4096, 0),
     ([8192, 3000, 1], 8, 4, 256, "f16", 64, 0, 0),       # head_dim 256 (register-staged kernel)
-    ([512, 40, 1000], 32, 8, 64, "f32", 32, 0, 0),       # the reference's f32 cache (VALU kernel)
+    ([512, 40, 1000], 32, 8, 64, "f32", 32, 0, 0),       # the reference's f32 cache (MFMA, f32 tiles)
     ([3000, 700], 12, 2, 128, "f32", 64, 333, 4),        # f32 with a binding window
+    ([33000, 12000], 32, 4, 128, "f32", 512, 4096, 0),   # f32, long context, binding window
+    ([9000, 20000, 3000, 1], 32, 4, 128, "f32", 256, 0, 0),  # f32, ragged batch
+    ([6000, 800], 16, 16, 64, "f32", 64, 0, 8),          # f32, head_dim 64, padded rows
+    ([3000, 1500], 8, 4, 256, "f32", 64, 0, 0),          # f32 at head_dim 256 (VALU kernel)
     ([9000, 2000], 16, 8, 256, "bf16", 256, 1024, 16),
 ]
 
@@ -97,8 +101,8 @@ def test_paged_vs_oracle(dev, case):
         assert_close(o[b].reshape(-1), ref[b], what=f"case {case} b={b}")
     if window == 0 and dt != "f32":
         # same blocks and splits as the contiguous path: identical bits (an
-        # f32 cache's contiguous short splits run on the MFMA block kernel,
-        # its pages on decode_split_kernel: both checked against the oracle)
+        # f32 cache's contiguous short splits run on the block kernel, its
+        # pages on decode_dma_kernel: both checked against the oracle)
         ws = A.new_decode_workspace(B, H, Hk, D, L_, 0, dev)
         oc = A.attn_decode(q, kc, vc, sl, L_, Hk, kv_stride=Hk * D + pad, seq_stride=L_ * (Hk * D + pad),
                            workspace=ws)

@@ -396,14 +396,21 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
     const int32_t *__restrict__ ptab, int ptab_stride, int page_shift, int n_pages) {
     constexpr int NS = D / 32;          // QK k-steps (32 d each)
     constexpr int NDT = D / 16;         // 16-wide d tiles of O^T
-    constexpr int RB = D * 2;           // bytes per key row of one head
-    constexpr int SLOTS = D / 8;        // 16-byte slots per row
+    // An f32 cache (the reference's) arrives as f32 tiles; both contractions
+    // then run on bf16 MFMAs over hi + lo halves, as in decode_block_kernel:
+    // Q.K = Khi.Qhi + Khi.Qlo + Klo.Qhi, P.V = Vhi.Phi + Vhi.Plo + Vlo.Phi.
+    constexpr bool F = __is_same(T, F32);
+    using MT = typename std::conditional<F, BF16, T>::type;  // MFMA operand type
+    constexpr int EB = T::bytes;        // cache element bytes
+    constexpr int RB = D * EB;          // bytes per key row of one head
+    constexpr int SLOTS = RB / 16;      // 16-byte slots per row
     constexpr int RPI = 1024 / RB;      // rows written by one DMA instruction
     constexpr int NI = kTok / RPI;      // DMA instructions per K (or V) tile
     constexpr int TILE = kTok * RB;     // bytes of one K (or V) tile
     constexpr int STAGE = 2 * TILE;     // K tile then V tile
-    constexpr bool SPLITP = __is_same(T, BF16);
+    constexpr bool SPLITP = !__is_same(T, F16);
     static_assert(D == 64 || D == 128, "DMA decode path covers head_dim 64 and 128");
+    static_assert(2 * MW * STAGE <= 160 * 1024, "two LDS stages per wave");
 
     const int split = blockIdx.x, unit = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -441,10 +448,10 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
     const int c0 = (fetch_len > 0 ? 0 : (PG ? start & ~(kTok - 1) : start)) + split * chunk;
     const int cf = fetch_len > 0 ? min(c0 + chunk, fetch_len) : min(c0 + chunk, len);
 
-    const int rb = (int)(kv_stride * 2);
-    const char *kb0 = kc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
-    const char *vb0 = vc + (int64_t)b * seq_stride * 2 + (int64_t)kvh * D * 2;
-    const int range = cf > 0 ? (cf - 1) * rb + D * 2 : 0;
+    const int rb = (int)(kv_stride * EB);
+    const char *kb0 = kc + (int64_t)b * seq_stride * EB + (int64_t)kvh * RB;
+    const char *vb0 = vc + (int64_t)b * seq_stride * EB + (int64_t)kvh * RB;
+    const int range = cf > 0 ? (cf - 1) * rb + RB : 0;
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kb0), 0, range, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t vrs =
@@ -466,7 +473,7 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
             // invalid page too: never read past the caller's table.
             const int phys = pg < ptab_stride ? ptab[(int64_t)b * ptab_stride + pg] : -1;
             const bool ok = phys >= 0 && phys < n_pages;
-            const int64_t pb = ((int64_t)(ok ? phys : 0) << page_shift) * rb + (int64_t)kvh * D * 2;
+            const int64_t pb = ((int64_t)(ok ? phys : 0) << page_shift) * rb + (int64_t)kvh * RB;
             const int prange = ok ? (rb << page_shift) : 0;
             const __amdgpu_buffer_rsrc_t kp =
                 __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kc + pb), 0, prange, kRsrcWord3);
@@ -517,7 +524,7 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
         for (int j = 0; j < 4; j++) {
             const float x0 = head_ok ? qa[s][j >> 1][(2 * j) & 3] * qscale : 0.f;
             const float x1 = head_ok ? qa[s][j >> 1][(2 * j + 1) & 3] * qscale : 0.f;
-            const u32x2 hl = split2<T>(x0, x1);
+            const u32x2 hl = split2<MT>(x0, x1);
             qh[s][j] = hl[0];
             ql[s][j] = hl[1];
         }
@@ -535,13 +542,17 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
         else __builtin_amdgcn_s_waitcnt(vm_wait(NI));
         // S^T = K . Q^T: lane (key t*16 + n16, chunk s*4 + kg)
         const uint32_t kbase = lds_addr(kt);
-        u32x4 ka[2 * NS];
+        constexpr int KR = F ? 2 : 1;  // 16-byte reads per operand
+        u32x4 ka[2 * NS * KR];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             const int r = t * 16 + n16;
 #pragma unroll
             for (int s = 0; s < NS; s++)
-                ka[t * NS + s] = lds_read_b128(kbase + r * RB + (((s * 4 + kg) ^ (r & (SLOTS - 1))) * 16));
+#pragma unroll
+                for (int h = 0; h < KR; h++)
+                    ka[(t * NS + s) * KR + h] =
+                        lds_read_b128(kbase + r * RB + ((((s * 4 + kg) * KR + h) ^ (r & (SLOTS - 1))) * 16));
         }
         lds_wait(ka);
         f32x4 sacc[2];
@@ -550,8 +561,24 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
             sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < NS; s++) {
-                sacc[t] = mfma16<T>(ka[t * NS + s], qh[s], sacc[t]);
-                sacc[t] = mfma16<T>(ka[t * NS + s], ql[s], sacc[t]);
+                if constexpr (F) {
+                    const u32x4 a = ka[(t * NS + s) * 2], c = ka[(t * NS + s) * 2 + 1];
+                    u32x4 kh, kl;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const u32x4 &src = j < 2 ? a : c;
+                        const u32x2 hl = split2<BF16>(__uint_as_float(src[(2 * j) & 3]),
+                                                      __uint_as_float(src[(2 * j + 1) & 3]));
+                        kh[j] = hl[0];
+                        kl[j] = hl[1];
+                    }
+                    sacc[t] = mfma16<BF16>(kh, qh[s], sacc[t]);
+                    sacc[t] = mfma16<BF16>(kh, ql[s], sacc[t]);
+                    sacc[t] = mfma16<BF16>(kl, qh[s], sacc[t]);
+                } else {
+                    sacc[t] = mfma16<T>(ka[t * NS + s], qh[s], sacc[t]);
+                    sacc[t] = mfma16<T>(ka[t * NS + s], ql[s], sacc[t]);
+                }
             }
         }
         float sv[8];
@@ -592,7 +619,7 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             if constexpr (SPLITP) {
-                const u32x2 hl = split2<T>(p[2 * j], p[2 * j + 1]);
+                const u32x2 hl = split2<MT>(p[2 * j], p[2 * j + 1]);
                 ph[j] = hl[0];
                 pl[j] = hl[1];
             } else {
@@ -617,6 +644,40 @@ __global__ __launch_bounds__(MW * 64, 1) void decode_dma_kernel(
         }
         // O^T += V^T . P^T; lane n16 of key group kg reads V rows kg*4 + n16/4
         // (+16), elements dt*16 + 4*(n16 % 4) .. +3, transposed by the read.
+        if constexpr (F) {
+            // V^T operand gathered from the f32 rows: lane (d = dt*16 + n16,
+            // kg) takes rows kg*4 + j and 16 + kg*4 + j (j < 4) of column d,
+            // then splits them into bf16 hi and lo halves.
+            const uint32_t vbase = lds_addr(vt);
+            float vv[NDT][8];
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                const int d = dt * 16 + n16;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int r = (j >> 2) * 16 + kg * 4 + (j & 3);
+                    vv[dt][j] = __uint_as_float(lds_read_b32(
+                        vbase + r * RB + (((d >> 2) ^ (r & (SLOTS - 1))) * 16) + (d & 3) * 4));
+                }
+            }
+            lds_wait_any();
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) tie_f(vv[dt][j]);
+                u32x4 vh, vl;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const u32x2 hl = split2<BF16>(vv[dt][2 * j], vv[dt][2 * j + 1]);
+                    vh[j] = hl[0];
+                    vl[j] = hl[1];
+                }
+                oacc[dt] = mfma16<BF16>(vh, ph, oacc[dt]);
+                oacc[dt] = mfma16<BF16>(vh, pl, oacc[dt]);
+                oacc[dt] = mfma16<BF16>(vl, ph, oacc[dt]);
+            }
+            return;
+        }
         const int vr0 = kg * 4 + (n16 >> 2);
         const uint32_t vbase = lds_addr(vt);
         u32x4 va[NDT];
@@ -1093,7 +1154,7 @@ static const int kEnvSplitsM = env_override("ULLM_HIP_DECODE_SPLITS");
 static const bool kNoBlock = env_override("ULLM_HIP_DECODE_NOBLOCK") == 1;
 
 static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_len, int window,
-                          bool paged = false) {
+                          bool paged = false, int eb = 2) {
     MfmaPlan p{};
     const int kv_mul = n_head / n_kv_head;
     p.gt = kv_mul;
@@ -1117,6 +1178,9 @@ static MfmaPlan plan_mfma(int batch, int n_head, int n_kv_head, int D, int max_l
     if (D > 128 || whole) p.mw = kMW;
     else p.mw = (int64_t)units * blocks <= 1024 ? 1 : 2;
     if (D <= 128 && (kEnvMw == 1 || kEnvMw == 2 || kEnvMw == kMW)) p.mw = kEnvMw;  // tuning override
+    // An f32 cache at head_dim 128: two 32 KB stages per wave, so at most two
+    // waves per workgroup fit the LDS.
+    if (eb == 4 && D == 128 && p.mw > 2) p.mw = 2;
     const int tile = p.mw * kTok;
     int splits = (visible + tile - 1) / tile;
     int want = (kMfmaTargetWG * (p.mw == kMW ? 1 : 2) + units - 1) / units;
@@ -1188,8 +1252,10 @@ struct MainLaunch {
     static void run(int mw, dim3 g, hipStream_t st, A... a) {
         const int32_t *nt = nullptr;
         if (mw == 1) hipLaunchKernelGGL((decode_dma_kernel<T, D, 1>), g, dim3(64), 0, st, a..., nt, 0, 0, 0);
-        else if (mw == 2) hipLaunchKernelGGL((decode_dma_kernel<T, D, 2>), g, dim3(128), 0, st, a..., nt, 0, 0, 0);
-        else hipLaunchKernelGGL((decode_dma_kernel<T, D, kMW>), g, dim3(kMW * 64), 0, st, a..., nt, 0, 0, 0);
+        else if (mw == 2 || (__is_same(T, F32) && D == 128))  // f32 at head_dim 128: at most 2 waves
+            hipLaunchKernelGGL((decode_dma_kernel<T, D, 2>), g, dim3(128), 0, st, a..., nt, 0, 0, 0);
+        else if constexpr (!(__is_same(T, F32) && D == 128))
+            hipLaunchKernelGGL((decode_dma_kernel<T, D, kMW>), g, dim3(kMW * 64), 0, st, a..., nt, 0, 0, 0);
     }
 };
 template <class T, int D>
@@ -1283,7 +1349,7 @@ static void launch_mfma(const MfmaPlan &p, const float *q, const void *kc, const
             return;
         }
     }
-    if constexpr (__is_same(T, F32)) return;  // f32 comes here only for block plans
+    if constexpr (__is_same(T, F32) && D > 128) return;  // f32 head_dim 256: decode.hip
     else {
     MainLaunch<T, D>::run(p.mw, dim3(p.splits, p.n_units, batch), st, q, (const char *)kc,
                           (const char *)vc, kvs, ss, lens, win, fetch_len, nh, kv_mul, p.gt,
@@ -1299,15 +1365,14 @@ size_t decode_mfma_plan_bytes(int batch, int n_head, int n_kv_head, int D, int m
     return plan_mfma(batch, n_head, n_kv_head, D, max_len, window).bytes;
 }
 
-// The reference's f32 cache on decode_block_kernel, where the f16/bf16 plan
-// cuts one- or two-block splits (head_dim 64/128, contiguous cache); *bytes
-// is that plan's workspace.  Other f32 requests stay on decode_split_kernel.
+// The reference's f32 cache at head_dim 64 and 128 runs on the MFMA kernels
+// (decode_block_kernel for one- and two-block splits, decode_dma_kernel for
+// longer ones); *bytes is that plan's workspace.  head_dim 256 stays on
+// decode_split_kernel (decode.hip).
 bool decode_f32_block_plan(int batch, int n_head, int n_kv_head, int D, int max_len, int window,
                            size_t *bytes) {
-    if (D > 128 || kNoBlock) return false;
-    const MfmaPlan p = plan_mfma(batch, n_head, n_kv_head, D, max_len, window);
-    if (!(p.mw == 1 && (p.chunk == kTok || p.chunk == 2 * kTok) && p.splits > 1)) return false;
-    *bytes = p.bytes;
+    if (D > 128) return false;
+    *bytes = plan_mfma(batch, n_head, n_kv_head, D, max_len, window, false, 4).bytes;
     return true;
 }
 
@@ -1315,7 +1380,7 @@ int decode_mfma(int dtype, const float *q, const void *kc, const void *vc, int64
                 int64_t ss, const int32_t *lens, int max_len, int win, int batch, int nh,
                 int nkv, int D, float qs, float *out, void *ws, size_t ws_bytes,
                 hipStream_t st) {
-    const MfmaPlan p = plan_mfma(batch, nh, nkv, D, max_len, win);
+    const MfmaPlan p = plan_mfma(batch, nh, nkv, D, max_len, win, false, dtype_bytes(dtype));
     if (p.bytes > 0 && (!ws || ws_bytes < p.bytes))
         return set_error(ULLM_HIP_E_WORKSPACE, "decode: workspace of %zu bytes needed, %zu given",
                          p.bytes, ws_bytes);
@@ -1383,6 +1448,7 @@ static void launch_paged(const MfmaPlan &p, const float *q, const void *kp, cons
         };
         if (p.mw == 1) go(Int<1>{});
         else if (p.mw == 2) go(Int<2>{});
+        else if constexpr (__is_same(T, F32) && D == 128) go(Int<2>{});
         else go(Int<kMW>{});
     }
     if (p.splits > 1) launch_merge<D>(p, batch, nh, out, ws, st);
@@ -1434,13 +1500,15 @@ extern "C" int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, c
         return set_error(ULLM_HIP_E_INVALID, "decode_paged: null tensor pointer");
     if (((uintptr_t)k_pages | (uintptr_t)v_pages | (uintptr_t)q) & 15)
         return set_error(ULLM_HIP_E_INVALID, "decode_paged: q/k_pages/v_pages must be 16-byte aligned");
-    if (kv_dtype == ULLM_DT_F32)
+    // f32 pages at head_dim 256 run on the VALU split kernel (decode.hip);
+    // every other shape on the MFMA kernels.
+    if (kv_dtype == ULLM_DT_F32 && head_dim > 128)
         return decode_f32_paged(q, k_pages, v_pages, kv_stride, block_table, table_stride,
                                 __builtin_ctz(page_size), n_pages, seq_lens, max_len, window,
                                 batch, n_head, n_kv_head, head_dim, scale * kLog2e, out, workspace,
                                 workspace_bytes, (hipStream_t)stream);
     const MfmaPlan p = plan_mfma(batch, n_head, n_kv_head, head_dim, max_len, paged_plan_window(window),
-                                 true);
+                                 true, dtype_bytes(kv_dtype));
     if (p.bytes > 0 && (!workspace || workspace_bytes < p.bytes))
         return set_error(ULLM_HIP_E_WORKSPACE, "decode_paged: workspace of %zu bytes needed, %zu given",
                          p.bytes, workspace_bytes);
@@ -1452,7 +1520,10 @@ extern "C" int ullm_hip_attn_decode_paged(const float *q, const void *k_pages, c
 #define ULLM_PAGED(TT, DD) \
     launch_paged<TT, DD>(p, q, k_pages, v_pages, kv_stride, block_table, table_stride, shift, n_pages, \
                          seq_lens, window, batch, n_head, kv_mul, qs, out, w, st)
-    if (kv_dtype == ULLM_DT_F16) {
+    if (kv_dtype == ULLM_DT_F32) {
+        if (head_dim == 64) ULLM_PAGED(F32, 64);
+        else ULLM_PAGED(F32, 128);
+    } else if (kv_dtype == ULLM_DT_F16) {
         if (head_dim == 64) ULLM_PAGED(F16, 64);
         else if (head_dim == 128) ULLM_PAGED(F16, 128);
         else ULLM_PAGED(F16, 256);

@@ -181,6 +181,14 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4 &a, const u32x4 &b, const f
 // wait so the compiler cannot use them earlier.
 __device__ __forceinline__ void lds_wait_any() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 __device__ __forceinline__ void tie(u32x4 &r) { asm volatile("" : "+v"(r)); }
+__device__ __forceinline__ void tie_f(float &r) { asm volatile("" : "+v"(r)); }
+// One 4-byte LDS read per lane, not tracked by the compiler (see the 16-byte
+// reads above); the caller waits with lds_wait_any() and ties the result.
+__device__ __forceinline__ uint32_t lds_read_b32(uint32_t a) {
+    uint32_t r;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
 __device__ __forceinline__ void tie(u32x2 &r) { asm volatile("" : "+v"(r)); }
 
 // Workgroup barrier without a memory fence (LDS DMA visibility is ensured by

@@ -113,7 +113,7 @@ __global__ __launch_bounds__(512) void prefill2_kernel(
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int half = wave >> 2, slot = wave & 3;
+    const int slot = wave & 3;
     const int kv_len = start_pos + S;
 
     // Key range of one wave (uniform): rows of block (group, slot).

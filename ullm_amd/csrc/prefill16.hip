@@ -309,9 +309,12 @@ __global__ __launch_bounds__(512, OCC) void prefill16_kernel(
         u32x4 vb[NDT];
         auto rdv = [&](auto dtc) {
             constexpr int dt = decltype(dtc)::value;
-            const u32x2 lo = lds_read_tr16_b64_at<(dt >> 3) * 256>(vaddr[dt & 7]);
-            const u32x2 hi = lds_read_tr16_b64_at<(dt >> 3) * 256 + 16 * RBV>(vaddr[dt & 7]);
-            vb[dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+            // (the reads of d tiles 8-15 are named only where NDT is 16)
+            if constexpr (dt < NDT) {
+                const u32x2 lo = lds_read_tr16_b64_at<(dt >> 3) * 256>(vaddr[dt & 7]);
+                const u32x2 hi = lds_read_tr16_b64_at<(dt >> 3) * 256 + 16 * RBV>(vaddr[dt & 7]);
+                vb[dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+            }
         };
         if constexpr (F) {
             // K hi and lo in batches of 8 operands each (head_dim 256: two
