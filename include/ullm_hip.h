@@ -258,8 +258,8 @@ int ullm_hip_qkv_append_paged(const float *q_in, const float *k_in, const float 
  * ullm_hip_attn_prefill on the gathered cache: chunked prefill of a
  * sequence whose earlier positions are already in pages.  No counterpart in
  * the reference (contiguous cache, lib.rs:184-185).  page_size: a power of
- * two >= 64; head_dim 64, 128 or 256 with f16/bf16 pages, head_dim 128 or
- * 256 with f32 pages and f32 q (else ULLM_HIP_E_UNSUPPORTED).
+ * two >= 64; head_dim 64, 128 or 256 with f16, bf16 or f32 pages (q in the
+ * pages' dtype; else ULLM_HIP_E_UNSUPPORTED).
  * Pages outside [0, n_pages) read as zeros. */
 int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, const void *v_pages,
                                 int dtype, int64_t kv_stride, int page_size, int n_pages,

@@ -202,7 +202,7 @@ def test_paged_prefill_validation():
         a.update(kw)
         return f(*a.values())
 
-    assert call(dt=L.DT_F32, d=64) == L.E_UNSUPPORTED   # f32 pages: head_dim 128 or 256
+    assert call(dt=L.DT_F32, d=64) == L.E_INVALID       # f32 pages at every head_dim; null pointers
     assert call(dt=L.DT_F32) == L.E_INVALID              # accepted; then the null pointers
     assert call(dt=L.DT_F16, kvs=1028) == L.E_INVALID    # 2056-byte rows: not
     assert call(d=96) == L.E_UNSUPPORTED

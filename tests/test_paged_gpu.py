@@ -260,6 +260,9 @@ PREFILL_CASES = [
     (2048, 0, 32, 8, 128, "f32", 256, 0),       # f32, cfg3 shape, one key stream
     (200, 700, 12, 4, 128, "f32", 128, 250),    # f32, chunked, binding window, 1 head per workgroup
     (500, 300, 8, 4, 256, "f32", 64, 0),        # f32 at head_dim 256, chunked
+    (700, 0, 32, 8, 64, "f32", 64, 0),          # f32 at head_dim 64 (prefill_f32_kernel)
+    (300, 500, 16, 4, 64, "f32", 128, 200),     # f32 at head_dim 64, chunked, binding window
+    (97, 31, 6, 2, 64, "f32", 64, 0),           # f32 at head_dim 64, ragged tail, 3:1 GQA
 ]
 
 

@@ -160,7 +160,7 @@ def attn_prefill_paged(q, k_pages, v_pages, block_table, n_head, n_kv_head, head
     """Causal prefill of S rows (positions start_pos..) of one sequence whose
     keys live in pages: block_table int32 [table_len] (page of key t =
     block_table[t // page_size]).  q: [S, n_head*head_dim] f16/bf16, or f32
-    with f32 pages at head_dim 128 or 256."""
+    with f32 pages (head_dim 64, 128 or 256)."""
     S = q.shape[0]
     _need_cuda(q, k_pages, v_pages, block_table)
     if not q.is_contiguous() or q.numel() != S * n_head * head_dim:

@@ -1242,7 +1242,7 @@ template <int D, int NRAW = 2>
 __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
     int64_t kv_stride, int S, int start_pos, int window, int n_head, int kv_mul, int hw,
-    int n_units, int n_pairs, float qscale, float *__restrict__ out) {
+    int n_units, int n_pairs, float qscale, float *__restrict__ out, KvPages pgs) {
     constexpr int BN = 32, RB = D * 2, KP = D * 2 + 16;  // keys per tile; f16/bf16 row bytes; K pitch
     constexpr int NKS = D / 16, NDT = D / 32;
     constexpr int FPR = D / 4;              // 16-byte f32 chunks per cache row
@@ -1303,13 +1303,24 @@ __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(
     };
     // Thread tid loads chunks ci = tid + 256 i: row ci / FPR, f32 chunk ci % FPR.
     u32x4 kraw[NRAW][NCH], vraw[NRAW][NCH];
+    // Paged (pgs.tab): the tile's page gives the buffer resources (a tile
+    // never crosses a page; keys past the sequence, or pages outside the
+    // table or pool, read zeros).
     auto issue = [&](u32x4(&kr)[NCH], u32x4(&vr)[NCH], int j) {
-        const int so = step_off(j);
+        __amdgpu_buffer_rsrc_t kq = krs, vq = vrs;
+        int so;
+        if (pgs.tab) {
+            const char *kcb = (const char *)kc, *vcb = (const char *)vc;
+            page_tile<D, 4>(pgs, kcb, vcb, kvh, rbg, kv_len, j < nsteps ? tile_of(j) * BN : kv_len,
+                            kq, vq, so);
+        } else {
+            so = step_off(j);
+        }
 #pragma unroll
         for (int i = 0; i < NCH; i++) {
             const int ci = tid + 256 * i, off = (ci / FPR) * rbg + (ci % FPR) * 16 + so;
-            kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
-            vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
+            kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kq, off, 0, 0));
+            vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vq, off, 0, 0));
         }
     };
     const uint32_t lds0 = lds_addr(lds);
@@ -1552,7 +1563,7 @@ __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(
 template <int D>
 static int launch_prefill_f32(const void *q, const void *kc, const void *vc, int64_t kvs, int S,
                               int sp, int win, int nh, int kv_mul, float qs, float *out,
-                              hipStream_t st) {
+                              hipStream_t st, KvPages pgs = KvPages{}) {
     int hw = 1;
     while (hw < 4 && kv_mul % (hw * 2) == 0) hw *= 2;
     const int n_units = (S + 128 / hw - 1) / (128 / hw);
@@ -1561,7 +1572,7 @@ static int launch_prefill_f32(const void *q, const void *kc, const void *vc, int
     const int per_xcd = (total + 7) / 8;
     hipLaunchKernelGGL((prefill_f32_kernel<D>), dim3(per_xcd * 8), dim3(256), 0, st,
                        (const float *)q, (const float *)kc, (const float *)vc, kvs, S, sp, win,
-                       nh, kv_mul, hw, n_units, n_pairs, qs, out);
+                       nh, kv_mul, hw, n_units, n_pairs, qs, out, pgs);
     return check_hip(hipGetLastError(), "prefill (f32) launch");
 }
 
@@ -1631,9 +1642,8 @@ extern "C" int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, c
                                            int table_len, int S, int start_pos, int window,
                                            int n_head, int n_kv_head, int head_dim, float scale,
                                            float *out, void *stream) {
-    if (dtype != ULLM_DT_F16 && dtype != ULLM_DT_BF16 && !(dtype == ULLM_DT_F32 && head_dim != 64))
-        return set_error(ULLM_HIP_E_UNSUPPORTED,
-                         "prefill_paged: dtype %d at head_dim %d (f16/bf16; f32 at 128 or 256)", dtype, head_dim);
+    if (!dtype_ok(dtype))
+        return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: dtype %d", dtype);
     if (head_dim != 64 && head_dim != 128 && head_dim != 256)
         return set_error(ULLM_HIP_E_UNSUPPORTED, "prefill_paged: head_dim %d not in {64,128,256}", head_dim);
     if (n_head < 1 || n_kv_head < 1 || n_head % n_kv_head || S < 0 || start_pos < 0)
@@ -1663,7 +1673,10 @@ extern "C" int ullm_hip_attn_prefill_paged(const void *q, const void *k_pages, c
     const float qs = scale * kLog2e;
     const int kv_mul = n_head / n_kv_head;
     hipStream_t st = (hipStream_t)stream;
-    if (dtype == ULLM_DT_F32) {  // f32 pages: prefill16_kernel's f32 mode
+    if (dtype == ULLM_DT_F32) {  // f32 pages: prefill16_kernel's f32 mode, prefill_f32_kernel at 64
+        if (head_dim == 64)
+            return launch_prefill_f32<64>(q, k_pages, v_pages, kv_stride, S, start_pos, window, n_head,
+                                          kv_mul, qs, out, st, pgs);
         if (head_dim == 256)
             return launch_prefill16(ULLM_DT_F32, q, k_pages, v_pages, kv_stride, S, start_pos, window,
                                     n_head, kv_mul, qs, out, st, pgs);
