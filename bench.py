@@ -39,7 +39,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", choices=["all", "decode", "prefill", "long", "append", "proj",
-                                       "matmul", "paged", "cfg1", "cfg4", "f32prefill", "copy",
+                                       "matmul", "paged", "cfg1", "cfg4", "f32prefill", "f32decode",
+                                       "copy",
                                        "floor"],
                     default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -615,6 +616,11 @@ def main():
         res["f32_prefill_d256"] = bench_prefill(torch, A, args, 1024, 8, 4, 256, torch.float32)
     if want("cfg1"):
         res["cfg1"] = bench_decode(torch, A, args, 32, 8, 64, 512, 28, torch.float32, "cfg1")
+    if want("f32decode"):
+        # cfg5's shape over the reference's own f32 cache (128 MiB per layer).
+        res["f32_long"] = bench_decode(torch, A, argparse.Namespace(steps=max(5, args.steps // 10),
+                                                                    warmup=3),
+                                       32, 4, 128, 32768, 12, torch.float32, "f32_long")
     if want("cfg4"):
         # One step = a 6-layer group: 5 sliding-window layers (1024 keys) and
         # the global layer, at context 8192 (forward.rs:450-454 / lib.rs:1183-1186).
@@ -740,6 +746,15 @@ def main():
                             "tflops": round(res["f32_prefill_d256"]["tflops"], 2),
                             "frac_mfma": round(res["f32_prefill_d256"]["tflops"]
                                                / MFMA_BF16_PEAK_TFLOPS, 4)}},
+        "f32_long_decode": {"workload": "cfg5's shape (32/4 heads, head_dim 128, batch 1, 32768 "
+                                        "keys) over an f32 cache, the reference's own cache "
+                                        "dtype; 12 layers per graph",
+                            "kernel": "decode_dma_kernel<F32,128,2> (f32 tiles by LDS DMA, bf16 "
+                                      "hi + lo MFMAs) + decode_merge_kernel",
+                            "us_per_layer": round(res["f32_long"]["us_per_layer"], 3),
+                            "algorithmic_bytes": int(res["f32_long"]["layer_bytes"]),
+                            "gbps": round(res["f32_long"]["gbps_step"], 1),
+                            "frac_hbm": round(res["f32_long"]["gbps_step"] / HBM_PEAK_GBS, 4)},
         "long_decode": {"workload": "cfg5 Qwen3-30B-A3B-shaped decode, 32/4 heads, head_dim "
                                     "128, bf16 KV 32768, 48 layers",
                         "us_per_layer": round(lc["us_per_layer"], 3),
