@@ -120,7 +120,8 @@ size_t ullm_hip_decode_noalloc_max_bytes(void);
  * head_dim in {64, 128, 256}, for every dtype.  With an f32 cache (the
  * reference's own cache dtype) Q.K runs on bf16 hi + lo halves of Q and K (~2^-16 per product) and
  * V is rounded to f16.  For bf16 and f32 caches P.V runs in f16 (V is
- * converted to f16 on chip), so |V| must stay below 65504.  A layer's cache
+ * converted to f16 on chip), so |V| must stay below 65504 (beyond it the
+ * affected rows come out inf or NaN, never as wrong finite values).  A layer's cache
  * and q must each stay below 2 GiB (a longer prompt runs as chunks at
  * increasing start_pos). */
 int ullm_hip_attn_prefill(const void *q, const void *k_cache, const void *v_cache, int dtype,

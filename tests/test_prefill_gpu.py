@@ -340,3 +340,43 @@ def test_q_past_the_call_limit_runs_in_chunks(dev, monkeypatch, dtype, D):
                            window=120, rows=rows)
     assert_close(chunked.cpu().numpy(), ref, what="chunked")
     assert_close(chunked.cpu().numpy(), whole.cpu().numpy(), what="chunked vs one call")
+
+
+@pytest.mark.parametrize("dtype,S,H,Hk", [("bf16", 300, 8, 2), ("bf16", 2048, 32, 8), ("f32", 300, 8, 2)])
+def test_v_beyond_f16_range_fails_loudly(dev, dtype, S, H, Hk):
+    """P.V runs on f16 operands, so a bf16 or f32 cache holding |V| >= 65504
+    is outside the kernels' range (include/ullm_hip.h).  Pinned here: V up
+    to 6e4 stays within tolerance (relative to the output's scale), and one
+    V element of 1e5 never yields a wrong finite value: every output equals
+    the oracle or is non-finite (the overflowed element reaches the rows
+    whose key tiles contain it as inf or NaN)."""
+    D = 128
+    dt = {"bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+    print(f"[prefill] |V| edge {dtype} S{S} H{H} Hk{Hk}", flush=True)
+    q = synth.randn(31, 1, (S, H * D), dt).to(dev)
+    k = synth.randn(31, 2, (S, Hk * D), dt).to(dev)
+    v0 = synth.randn(31, 3, (S, Hk * D), torch.float32)
+    scale = 1.0 / math.sqrt(D)
+    rows = sample_rows(S, 31)
+    for big, loud in ((6.0e4, False), (1.0e5, True)):
+        v = v0.clone()
+        v[S // 3, 5] = big          # kv head 0, column 5
+        v[2 * S // 3, D + 17] = -big  # kv head 1, column 17
+        v = v.to(dt).to(dev)
+        out = A.attn_prefill(q, k, v, H, Hk, D, scale=scale)
+        torch.cuda.synchronize()
+        o = out.cpu().numpy()
+        ref = ora.attn_prefill(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                               v.float().cpu().numpy(), S, 0, H, Hk, D, scale, rows=rows)
+        o, ref = o[rows], ref[rows]
+        if not loud:
+            s = np.abs(ref).max()
+            assert np.all(np.isfinite(o))
+            assert np.abs(o - ref).max() <= 2e-3 * s
+            assert np.linalg.norm(o - ref) <= 1e-3 * np.linalg.norm(ref)
+        else:
+            fin = np.isfinite(o)
+            assert not fin.all(), "an element past f16's range must not vanish silently"
+            err = np.abs(np.where(fin, o, 0.0) - np.where(fin, ref, 0.0))
+            tol = 2e-3 * np.maximum(1.0, np.abs(ref))
+            assert np.all(err <= tol), "a finite output differs from the oracle"
