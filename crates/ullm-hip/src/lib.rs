@@ -333,7 +333,7 @@ impl HipAttention {
         ffi::check(unsafe {
             ffi::ullm_hip_qkv_append(
                 q, k, v, dev_f32(hp.q_bias), dev_f32(hp.k_bias), dev_f32(hp.v_bias),
-                dev_f32(hp.q_norm), dev_f32(hp.k_norm), p.eps, self.rope_cs.ptr.cast(),
+                dev_f32(hp.q_norm), dev_f32(hp.k_norm), p.eps, self.rope_cs.ptr as *const f32,
                 p.n_ctx as c_int, p.rope_neox as c_int, self.rd as c_int, rows as c_int,
                 start as c_int, p.n_head as c_int, p.n_kv_head as c_int, p.head_dim as c_int,
                 q_out, q_dtype, self.key_cache.at(off), self.val_cache.at(off), p.kv_dtype,
@@ -348,8 +348,8 @@ impl HipAttention {
         let off = self.layer_off(layer);
         ffi::check(unsafe {
             ffi::ullm_hip_attn_decode(
-                self.qprep.ptr.cast(), self.key_cache.at(off), self.val_cache.at(off),
-                p.kv_dtype, kd as i64, 0, self.lens.at(pos * 4).cast(), (pos + 1) as c_int,
+                self.qprep.ptr as *const f32, self.key_cache.at(off), self.val_cache.at(off),
+                p.kv_dtype, kd as i64, 0, self.lens.at(pos * 4) as *const i32, (pos + 1) as c_int,
                 self.window(layer), 1, p.n_head as c_int, p.n_kv_head as c_int,
                 p.head_dim as c_int, self.scale(), out, self.ws.ptr, self.ws_bytes, self.stream)
         })
@@ -481,7 +481,7 @@ impl HipAttention {
         log(stat("wk", k));
         log(stat("wv", v));
         let (qv, kv, vv) = self.stage(q, k, v, 1)?;
-        self.append(layer, 1, pos, hp, qv.ptr.cast(), kv.ptr.cast(), vv.ptr.cast(),
+        self.append(layer, 1, pos, hp, qv.ptr as *const f32, kv.ptr as *const f32, vv.ptr as *const f32,
                     self.qprep.ptr, ffi::ULLM_DT_F32)?;
         self.synchronize()?;
         let mut buf = vec![0f32; qd];
@@ -500,7 +500,7 @@ impl HipAttention {
             };
             log(stat(label, &vals));
         }
-        self.decode(layer, pos, self.host_out.ptr.cast())?;
+        self.decode(layer, pos, self.host_out.ptr as *mut f32)?;
         self.synchronize()?;
         self.host_out.download(&mut buf)?;
         log(stat("attn_out", &buf));
