@@ -90,3 +90,12 @@ def test_cfg3_prefill_prep(dev):
 def test_decode_single_row_far_position(dev):
     run_case(dev, 1, 32000, 32, 4, 128, 128, True, norm=True, bias=False, qdt="f32",
              kvdt="bf16")
+
+
+@pytest.mark.parametrize("H,Hk,D,rd,neox", [(6, 3, 64, 64, True), (5, 1, 128, 128, False),
+                                            (3, 3, 256, 256, True), (7, 7, 64, 32, False),
+                                            (9, 3, 128, 96, True)])
+def test_partial_head_groups(dev, H, Hk, D, rd, neox):
+    """Head counts that leave a kind's last group of 256/D heads partly empty
+    (the empty lanes must store nothing), with full and partial rotary."""
+    run_case(dev, 4, 3, H, Hk, D, rd, neox, norm=True, bias=True, qdt="f32", kvdt="bf16")

@@ -1,20 +1,15 @@
 // Fused Q/K/V preparation + KV-cache append, and the host RoPE table.
 //
-// A workgroup of kAppendWaves waves owns one token row; a row's head vectors
-// ("slots") are
-//   slots [0, n_head)                 -> a query head
-//   slots [n_head, n_head+n_kv_head)  -> a key head
-//   slots [.., n_head+2*n_kv_head)    -> a value head
-// and wave w takes slots w, w + kAppendWaves, ..., kBatch at a time with
-// every load of a batch issued before any is used (the kernel streams
-// ~4 x D x 4 bytes per head and is HBM-bound).  Each slot gets, in the
-// reference's order (crates/ullm-model/src/lib.rs:1027-1058, decode
-// :877-914): bias add, per-head RMSNorm (math.rs:82-86), RoPE
-// (math.rs:116-161) via the precomputed (cos, sin) table, then the store --
-// q to q_out, K/V straight into the cache slot of position start_pos + row.
-// A lane holds D/64 consecutive elements (one 8-byte load for D = 128);
-// RoPE partners are exchanged through the wave's own LDS row.  This
-// replaces the bias, rmsnorm_heads and rope_* Metal dispatches
+// qkv_append_kernel: a workgroup of kAppendWaves waves owns one token row.
+// Each head vector gets, in the reference's order
+// (crates/ullm-model/src/lib.rs:1027-1058, decode :877-914): bias add,
+// per-head RMSNorm (math.rs:82-86), RoPE (math.rs:116-161) via the
+// precomputed (cos, sin) table, then the store -- q to q_out, K/V straight
+// into the cache slot of position start_pos + row.  The kernel streams
+// ~4 x D x 4 bytes per head; its VALU work per element is what limits it
+// once the loads are in flight, so a lane holds the two halves of a RoPE
+// pair (SplitEpi) and one RMS reduction serves 256/D heads.
+// This replaces the bias, rmsnorm_heads and rope_* Metal dispatches
 // (forward.rs:416-447, :799-853; shader.metal:828-941) with one launch.
 #include <cmath>
 #include "common.hpp"
@@ -64,7 +59,7 @@ __device__ __forceinline__ void store_e(void *base, int64_t idx, const float (&x
 }
 
 constexpr int kAppendWaves = 4;
-constexpr int kBatch = 4;  // slots per wave with loads in flight together
+constexpr int kBatch = 3;  // groups per wave with loads in flight together
 
 // Per-lane state of the head epilogue of one token row: the (cos, sin) of
 // this lane's elements at the row's position and the Q/K norm weights.  A
@@ -180,6 +175,104 @@ struct PageMap {
     int stride, shift, n_pages, rope_n_pos;
 };
 
+// Head epilogue of qkv_append_kernel in its split-half lane layout: a head
+// vector of D elements is held by L = D/4 lanes, lane m of the head holding
+// elements {2m, 2m+1} (x[0], x[1]) and {D/2+2m, D/2+2m+1} (x[2], x[3]), so a
+// wave holds HPW = 256/D heads.  Both full-width RoPE pairings are then
+// inside the lane: NeoX pairs e with e + D/2 (x[0]/x[2], x[1]/x[3]),
+// interleaved pairs 2j with 2j+1 (x[0]/x[1], x[2]/x[3]); only partial rotary
+// goes through LDS.  The RMS sum is a group_sum over the head's L lanes, one
+// reduction for HPW heads.
+template <int D>
+struct SplitEpi {
+    static constexpr int L = D / 4, HPW = 64 / L;
+    int m, rotary_dim, half, neox;
+    float eps;
+    float rc[4], rs[4], wq[4], wk[4];
+    const float *q_norm, *k_norm;
+
+    // Element index of x[i] of lane m.
+    __device__ __forceinline__ static int elem(int m, int i) { return (i >> 1) * (D / 2) + 2 * m + (i & 1); }
+
+    __device__ __forceinline__ SplitEpi(const float *cs, int pos, int rotary_dim_, int neox_,
+                                        const float *qn, const float *kn, float eps_)
+        : m((int)(threadIdx.x & 63) % L), rotary_dim(rotary_dim_), half(rotary_dim_ / 2),
+          neox(neox_), eps(eps_), q_norm(qn), k_norm(kn) {
+        const float *cp = cs + (int64_t)pos * half * 2;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = elem(m, i);
+            const int j = e < rotary_dim ? (neox ? (e < half ? e : e - half) : e >> 1) : 0;
+            rc[i] = cp[2 * j];
+            rs[i] = cp[2 * j + 1];
+            wq[i] = q_norm ? q_norm[e] : 1.f;
+            wk[i] = k_norm ? k_norm[e] : 1.f;
+        }
+    }
+
+    // Per-head RMSNorm (math.rs:82-86) and RoPE (math.rs:116-161) of one head
+    // vector of KIND 0 (q) or 1 (k), in the reference's order, the bias
+    // already added.  lds_head: D floats private to this head of the wave,
+    // used only for partial-rotary pairs.
+    template <int KIND>
+    __device__ __forceinline__ void norm_rope(float (&x)[4], float *lds_head) const {
+        if (KIND == 0 ? q_norm != nullptr : k_norm != nullptr) {
+            float ss = x[0] * x[0];
+#pragma unroll
+            for (int i = 1; i < 4; i++) ss += x[i] * x[i];
+            ss = group_sum<L>(ss);
+            // v_rsq_f32 (~1 ulp) for (sum/n + eps).sqrt().recip()
+            const float inv = __builtin_amdgcn_rsqf(ss / (float)D + eps);
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[i] = x[i] * inv * (KIND == 0 ? wq[i] : wk[i]);
+        }
+        float y[4];
+        if (rotary_dim == D) {
+            // (a, b) a pair, a the lower element: a' = a*c - b*s, b' = a*s + b*c
+            // with (c, s) of the pair (equal in both lanes of the pair's table).
+            auto pair = [&](int a, int b) {
+                y[a] = x[a] * rc[a] - x[b] * rs[a];
+                y[b] = x[a] * rs[b] + x[b] * rc[b];
+            };
+            if (neox) {  // wave-uniform
+                pair(0, 2);
+                pair(1, 3);
+            } else {
+                pair(0, 1);
+                pair(2, 3);
+            }
+        } else {
+            // Partial rotary: the partner of each pair comes from LDS (LDS
+            // operations of one wave complete in order).
+#pragma unroll
+            for (int i = 0; i < 4; i++) lds_head[elem(m, i)] = x[i];
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int e = elem(m, i);
+                y[i] = x[i];
+                if (e < rotary_dim) {
+                    if (neox) {
+                        const int j = e < half ? e : e - half;
+                        const float a = lds_head[j], c = lds_head[j + half];
+                        y[i] = e < half ? a * rc[i] - c * rs[i] : a * rs[i] + c * rc[i];
+                    } else {
+                        const float a = lds_head[e & ~1], c = lds_head[e | 1];
+                        y[i] = (e & 1) ? a * rs[i] + c * rc[i] : a * rc[i] - c * rs[i];
+                    }
+                }
+            }
+            __builtin_amdgcn_wave_barrier();  // the row may be rewritten next
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) x[i] = y[i];
+    }
+};
+
+// One token row per workgroup.  The row's head vectors are taken in groups of
+// HPW heads of one kind (q heads, then K heads, then V heads; a kind's last
+// group may be partly empty), group g by wave g % kAppendWaves, kBatch groups
+// at a time with every load of a batch issued before any is used.
 template <int D, int QDT, int KVDT>
 __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
     const float *__restrict__ q_in, const float *__restrict__ k_in, const float *__restrict__ v_in,
@@ -188,11 +281,14 @@ __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
     const float *__restrict__ k_norm, float eps, const float *__restrict__ cs, int neox,
     int rotary_dim, int rows, int start_pos, int n_head, int n_kv_head, void *q_out,
     void *k_cache, void *v_cache, int64_t kv_stride, PageMap pm) {
-    constexpr int E = D / 64;
-    __shared__ float buf[kAppendWaves][D];
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: slot math in SGPRs
+    using Epi = SplitEpi<D>;
+    constexpr int L = Epi::L, HPW = Epi::HPW;
+    __shared__ float buf[kAppendWaves][HPW * D];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: group math in SGPRs
+    const int hl = (int)(threadIdx.x & 63) / L;                          // head of the lane within a group
     const int row = blockIdx.x;
-    const int slots = n_head + 2 * n_kv_head;
+    const int gq = (n_head + HPW - 1) / HPW, gk = (n_kv_head + HPW - 1) / HPW;
+    const int groups = gq + 2 * gk;
     const int64_t q_dim = (int64_t)n_head * D, kv_dim = (int64_t)n_kv_head * D;
     int pos = start_pos + row;
     int64_t crow = pos;
@@ -204,37 +300,61 @@ __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
         if (phys < 0 || phys >= pm.n_pages) return;
         crow = ((int64_t)phys << pm.shift) + (pos & ((1 << pm.shift) - 1));
     }
-    const HeadEpi<D> epi(cs, pos, rotary_dim, neox, q_norm, k_norm, eps);
-    const int e0 = epi.e0;
+    const Epi epi(cs, pos, rotary_dim, neox, q_norm, k_norm, eps);
+    const int c0 = 2 * epi.m, c1 = D / 2 + 2 * epi.m;  // element offsets of x[0..1], x[2..3]
+    const unsigned loff = (unsigned)(hl * D + c0);      // of x[0..1] from the group's first head
+    const bool has_bias = q_bias || k_bias || v_bias;
 
-    for (int s0 = wave; s0 < slots; s0 += kAppendWaves * kBatch) {
-        float x[kBatch][E], bv[kBatch][E];
+    for (int g0 = wave; g0 < groups; g0 += kAppendWaves * kBatch) {
+        float x[kBatch][4], bv[kBatch][4];
         int kind[kBatch], head[kBatch];
+        bool ok[kBatch];
 #pragma unroll
         for (int b = 0; b < kBatch; b++) {
-            const int slot = s0 + b * kAppendWaves;
-            const bool ok = slot < slots;
-            kind[b] = !ok ? 3 : (slot < n_head ? 0 : (slot < n_head + n_kv_head ? 1 : 2));
-            head[b] = kind[b] == 0 ? slot : (kind[b] == 1 ? slot - n_head : slot - n_head - n_kv_head);
-            const float *src = kind[b] == 0 ? q_in + row * q_dim : (kind[b] == 1 ? k_in : v_in) + row * kv_dim;
+            const int g = g0 + b * kAppendWaves;
+            kind[b] = g < gq ? 0 : (g < gq + gk ? 1 : (g < groups ? 2 : 3));  // wave-uniform
+            const int first = kind[b] == 0 ? 0 : (kind[b] == 1 ? gq : gq + gk);
+            const int h0 = (g - first) * HPW;  // wave-uniform first head of the group
+            head[b] = h0 + hl;
+            ok[b] = kind[b] != 3 && head[b] < (kind[b] == 0 ? n_head : n_kv_head);
+            // uniform base + a 32-bit lane offset; a lane past the kind's last
+            // head re-reads head h0 (in bounds) and stores nothing
+            const float *src = (kind[b] == 0 ? q_in + row * q_dim : (kind[b] == 1 ? k_in : v_in) + row * kv_dim) + (int64_t)h0 * D;
             const float *bias = kind[b] == 0 ? q_bias : (kind[b] == 1 ? k_bias : v_bias);
-            if (ok) load_e<E>(src + (int64_t)head[b] * D + e0, x[b]);
-            else
-#pragma unroll
-                for (int i = 0; i < E; i++) x[b][i] = 0.f;
-            if (ok && bias) load_e<E>(bias + (int64_t)head[b] * D + e0, bv[b]);
-            else
-#pragma unroll
-                for (int i = 0; i < E; i++) bv[b][i] = 0.f;
+            const unsigned lo = ok[b] ? loff : (unsigned)c0;
+            float2 a{0.f, 0.f}, c{0.f, 0.f}, ba{0.f, 0.f}, bc{0.f, 0.f};
+            if (kind[b] != 3) {
+                a = *(const float2 *)(src + lo);
+                c = *(const float2 *)(src + lo + D / 2);
+                if (bias) {
+                    ba = *(const float2 *)(bias + (int64_t)h0 * D + lo);
+                    bc = *(const float2 *)(bias + (int64_t)h0 * D + lo + D / 2);
+                }
+            }
+            x[b][0] = a.x, x[b][1] = a.y, x[b][2] = c.x, x[b][3] = c.y;
+            bv[b][0] = ba.x, bv[b][1] = ba.y, bv[b][2] = bc.x, bv[b][3] = bc.y;
         }
 #pragma unroll
         for (int b = 0; b < kBatch; b++) {
             if (kind[b] == 3) continue;  // wave-uniform
+            if (has_bias)
 #pragma unroll
-            for (int i = 0; i < E; i++) x[b][i] += bv[b][i];
-            epi.norm_rope(x[b], kind[b], buf[wave]);
-            store_head<D, QDT, KVDT>(x[b], kind[b], head[b], row, crow, e0, q_dim, q_out, k_cache,
-                                     v_cache, kv_stride);
+                for (int i = 0; i < 4; i++) x[b][i] += bv[b][i];
+            if (kind[b] == 0) epi.template norm_rope<0>(x[b], &buf[wave][hl * D]);
+            else if (kind[b] == 1) epi.template norm_rope<1>(x[b], &buf[wave][hl * D]);
+            if (!ok[b]) continue;
+            const float lo[2] = {x[b][0], x[b][1]}, hi[2] = {x[b][2], x[b][3]};
+            const int h0 = head[b] - hl;  // wave-uniform
+            if (kind[b] == 0) {
+                void *dst = (char *)q_out + (row * q_dim + (int64_t)h0 * D) * (QDT == ULLM_DT_F32 ? 4 : 2);
+                store_e<QDT, 2>(dst, loff, lo);
+                store_e<QDT, 2>(dst, loff + D / 2, hi);
+            } else {
+                void *dst = (char *)(kind[b] == 1 ? k_cache : v_cache) +
+                            (crow * kv_stride + (int64_t)h0 * D) * (KVDT == ULLM_DT_F32 ? 4 : 2);
+                store_e<KVDT, 2>(dst, loff, lo);
+                store_e<KVDT, 2>(dst, loff + D / 2, hi);
+            }
         }
     }
 }
