@@ -365,7 +365,7 @@ __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
 // matvecs into q and the cache slot, bias, q/k norm and RoPE,
 // forward.rs:415-447): y = W x per head vector, W row-major [out][in_dim] in
 // f32, f16 or bf16 (math.rs:9-21 matvec_q: dequantised row times x, f32
-// sums), then the same head epilogue as qkv_append_kernel.
+// sums), then the head epilogue HeadEpi (bias, norm, RoPE, store).
 //
 // A workgroup owns one head vector (slot) of one token row: its
 // kProjWaves waves each compute D/kProjWaves rows of W, every lane
