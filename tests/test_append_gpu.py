@@ -92,10 +92,13 @@ def test_decode_single_row_far_position(dev):
              kvdt="bf16")
 
 
-@pytest.mark.parametrize("H,Hk,D,rd,neox", [(6, 3, 64, 64, True), (5, 1, 128, 128, False),
-                                            (3, 3, 256, 256, True), (7, 7, 64, 32, False),
-                                            (9, 3, 128, 96, True)])
-def test_partial_head_groups(dev, H, Hk, D, rd, neox):
+@pytest.mark.parametrize("rows,H,Hk,D,rd,neox", [(4, 6, 3, 64, 64, True), (4, 5, 1, 128, 128, False),
+                                                 (4, 3, 3, 256, 256, True), (4, 7, 7, 64, 32, False),
+                                                 (4, 9, 3, 128, 96, True), (3, 42, 6, 64, 64, False),
+                                                 (300, 5, 1, 128, 128, True)])
+def test_partial_head_groups(dev, rows, H, Hk, D, rd, neox):
     """Head counts that leave a kind's last group of 256/D heads partly empty
-    (the empty lanes must store nothing), with full and partial rotary."""
-    run_case(dev, 4, 3, H, Hk, D, rd, neox, norm=True, bias=True, qdt="f32", kvdt="bf16")
+    (the empty lanes must store nothing), with full and partial rotary; few
+    rows spread a row's groups over several workgroups (42/6 heads at D 64:
+    15 groups, a full part and a partial one), many rows keep one per row."""
+    run_case(dev, rows, 3, H, Hk, D, rd, neox, norm=True, bias=True, qdt="f32", kvdt="bf16")

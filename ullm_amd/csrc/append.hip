@@ -60,6 +60,7 @@ __device__ __forceinline__ void store_e(void *base, int64_t idx, const float (&x
 
 constexpr int kAppendWaves = 4;
 constexpr int kBatch = 3;  // groups per wave with loads in flight together
+constexpr int kAppendSplitBelow = 256;  // rows under which a row's groups spread over workgroups
 
 // Per-lane state of the head epilogue of one token row: the (cos, sin) of
 // this lane's elements at the row's position and the Q/K norm weights.  A
@@ -280,7 +281,7 @@ __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
     const float *__restrict__ v_bias, const float *__restrict__ q_norm,
     const float *__restrict__ k_norm, float eps, const float *__restrict__ cs, int neox,
     int rotary_dim, int rows, int start_pos, int n_head, int n_kv_head, void *q_out,
-    void *k_cache, void *v_cache, int64_t kv_stride, PageMap pm) {
+    void *k_cache, void *v_cache, int64_t kv_stride, PageMap pm, int gpw) {
     using Epi = SplitEpi<D>;
     constexpr int L = Epi::L, HPW = Epi::HPW;
     __shared__ float buf[kAppendWaves][HPW * D];
@@ -305,14 +306,17 @@ __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
     const unsigned loff = (unsigned)(hl * D + c0);      // of x[0..1] from the group's first head
     const bool has_bias = q_bias || k_bias || v_bias;
 
-    for (int g0 = wave; g0 < groups; g0 += kAppendWaves * kBatch) {
+    // This workgroup's groups: [gbeg, gend) of the row (gpw per workgroup
+    // along blockIdx.y; all of them when gridDim.y == 1).
+    const int gbeg = (int)blockIdx.y * gpw, gend = min(groups, gbeg + gpw);
+    for (int g0 = gbeg + wave; g0 < gend; g0 += kAppendWaves * kBatch) {
         float x[kBatch][4], bv[kBatch][4];
         int kind[kBatch], head[kBatch];
         bool ok[kBatch];
 #pragma unroll
         for (int b = 0; b < kBatch; b++) {
             const int g = g0 + b * kAppendWaves;
-            kind[b] = g < gq ? 0 : (g < gq + gk ? 1 : (g < groups ? 2 : 3));  // wave-uniform
+            kind[b] = g >= gend ? 3 : (g < gq ? 0 : (g < gq + gk ? 1 : 2));  // wave-uniform
             const int first = kind[b] == 0 ? 0 : (kind[b] == 1 ? gq : gq + gk);
             const int h0 = (g - first) * HPW;  // wave-uniform first head of the group
             head[b] = h0 + hl;
@@ -529,13 +533,13 @@ static void launch_kv(int kvdt, dim3 g, dim3 b, hipStream_t st, const float *qi,
                       const float *vi, const float *qb, const float *kb, const float *vb,
                       const float *qn, const float *kn, float eps, const float *cs, int neox,
                       int rd, int rows, int sp, int nh, int nkv, void *qo, void *kc, void *vc,
-                      int64_t kvs, PageMap pm) {
+                      int64_t kvs, PageMap pm, int gpw) {
     if (kvdt == ULLM_DT_F32)
-        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_F32>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
+        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_F32>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm, gpw);
     else if (kvdt == ULLM_DT_F16)
-        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_F16>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
+        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_F16>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm, gpw);
     else
-        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_BF16>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
+        hipLaunchKernelGGL((qkv_append_kernel<D, QDT, ULLM_DT_BF16>), g, b, 0, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm, gpw);
 }
 
 template <int D>
@@ -543,10 +547,24 @@ static void launch_q(int qdt, int kvdt, dim3 g, dim3 b, hipStream_t st, const fl
                      const float *ki, const float *vi, const float *qb, const float *kb,
                      const float *vb, const float *qn, const float *kn, float eps,
                      const float *cs, int neox, int rd, int rows, int sp, int nh, int nkv,
-                     void *qo, void *kc, void *vc, int64_t kvs, PageMap pm) {
-    if (qdt == ULLM_DT_F32) launch_kv<D, ULLM_DT_F32>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
-    else if (qdt == ULLM_DT_F16) launch_kv<D, ULLM_DT_F16>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
-    else launch_kv<D, ULLM_DT_BF16>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm);
+                     void *qo, void *kc, void *vc, int64_t kvs, PageMap pm, int gpw) {
+    if (qdt == ULLM_DT_F32) launch_kv<D, ULLM_DT_F32>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm, gpw);
+    else if (qdt == ULLM_DT_F16) launch_kv<D, ULLM_DT_F16>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm, gpw);
+    else launch_kv<D, ULLM_DT_BF16>(kvdt, g, b, st, qi, ki, vi, qb, kb, vb, qn, kn, eps, cs, neox, rd, rows, sp, nh, nkv, qo, kc, vc, kvs, pm, gpw);
+}
+
+// Grid of qkv_append_kernel: one token row per blockIdx.x; a row's head
+// groups spread over blockIdx.y in parts of gpw groups.  Few rows (decode, a
+// short chunk) leave CUs idle and each workgroup's waves would run several
+// rounds of loads, so each part is one round (kAppendWaves * kBatch groups);
+// many rows keep a row per workgroup.
+static dim3 append_grid(int rows, int n_head, int n_kv_head, int head_dim, int &gpw) {
+    static const int env = env_override("ULLM_HIP_APPEND_GPW");  // tuning override
+    const int hpw = 256 / head_dim;
+    const int groups = (n_head + hpw - 1) / hpw + 2 * ((n_kv_head + hpw - 1) / hpw);
+    gpw = rows < kAppendSplitBelow ? kAppendWaves * kBatch : groups;
+    if (env > 0) gpw = env;
+    return dim3((unsigned)rows, (unsigned)((groups + gpw - 1) / gpw));
 }
 
 }  // namespace ullm
@@ -602,12 +620,13 @@ extern "C" int ullm_hip_qkv_append(const float *q_in, const float *k_in, const f
                          rope_n_pos, start_pos + rows);
     if (q_out == (void *)q_in && q_dtype != ULLM_DT_F32)
         return set_error(ULLM_HIP_E_INVALID, "qkv_append: in-place q needs q_dtype f32");
-    dim3 grid((unsigned)rows), block(kAppendWaves * 64);
+    int gpw;
+    const dim3 grid = append_grid(rows, n_head, n_kv_head, head_dim, gpw), block(kAppendWaves * 64);
     hipStream_t st = (hipStream_t)stream;
     switch (head_dim) {
-        case 64: launch_q<64>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride, PageMap{}); break;
-        case 128: launch_q<128>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride, PageMap{}); break;
-        default: launch_q<256>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride, PageMap{}); break;
+        case 64: launch_q<64>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride, PageMap{}, gpw); break;
+        case 128: launch_q<128>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride, PageMap{}, gpw); break;
+        default: launch_q<256>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, start_pos, n_head, n_kv_head, q_out, k_cache, v_cache, kv_stride, PageMap{}, gpw); break;
     }
     return check_hip(hipGetLastError(), "qkv_append launch");
 }
@@ -646,12 +665,13 @@ extern "C" int ullm_hip_qkv_append_paged(const float *q_in, const float *k_in, c
         return set_error(ULLM_HIP_E_INVALID, "qkv_append_paged: in-place q needs q_dtype f32");
     const PageMap pm{positions, block_table, table_stride, __builtin_ctz(page_size), n_pages,
                      rope_n_pos};
-    dim3 grid((unsigned)rows), block(kAppendWaves * 64);
+    int gpw;
+    const dim3 grid = append_grid(rows, n_head, n_kv_head, head_dim, gpw), block(kAppendWaves * 64);
     hipStream_t st = (hipStream_t)stream;
     switch (head_dim) {
-        case 64: launch_q<64>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, 0, n_head, n_kv_head, q_out, k_pages, v_pages, kv_stride, pm); break;
-        case 128: launch_q<128>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, 0, n_head, n_kv_head, q_out, k_pages, v_pages, kv_stride, pm); break;
-        default: launch_q<256>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, 0, n_head, n_kv_head, q_out, k_pages, v_pages, kv_stride, pm); break;
+        case 64: launch_q<64>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, 0, n_head, n_kv_head, q_out, k_pages, v_pages, kv_stride, pm, gpw); break;
+        case 128: launch_q<128>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, 0, n_head, n_kv_head, q_out, k_pages, v_pages, kv_stride, pm, gpw); break;
+        default: launch_q<256>(q_dtype, kv_dtype, grid, block, st, q_in, k_in, v_in, q_bias, k_bias, v_bias, q_norm, k_norm, eps, rope_cs, rope_neox, rotary_dim, rows, 0, n_head, n_kv_head, q_out, k_pages, v_pages, kv_stride, pm, gpw); break;
     }
     return check_hip(hipGetLastError(), "qkv_append_paged launch");
 }
