@@ -270,10 +270,11 @@ struct SplitEpi {
     }
 };
 
-// One token row per workgroup.  The row's head vectors are taken in groups of
-// HPW heads of one kind (q heads, then K heads, then V heads; a kind's last
-// group may be partly empty), group g by wave g % kAppendWaves, kBatch groups
-// at a time with every load of a batch issued before any is used.
+// Token row blockIdx.x; the row's head vectors are taken in groups of HPW
+// heads of one kind (q heads, then K heads, then V heads; a kind's last group
+// may be partly empty), groups [blockIdx.y * gpw, +gpw) by this workgroup,
+// group g by wave g % kAppendWaves, kBatch groups at a time with every load
+// of a batch issued before any is used.
 template <int D, int QDT, int KVDT>
 __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
     const float *__restrict__ q_in, const float *__restrict__ k_in, const float *__restrict__ v_in,
