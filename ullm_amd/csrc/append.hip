@@ -372,13 +372,17 @@ __global__ __launch_bounds__(kAppendWaves * 64) void qkv_append_kernel(
 // f32, f16 or bf16 (math.rs:9-21 matvec_q: dequantised row times x, f32
 // sums), then the head epilogue HeadEpi (bias, norm, RoPE, store).
 //
-// A workgroup owns one head vector (slot) of one token row: its
-// kProjWaves waves each compute D/kProjWaves rows of W, every lane
-// accumulating 16-byte chunks of a row in f32 with x's matching chunk
-// (loaded once per chunk for all of the wave's rows), then a wave sum per
-// row.  The D results meet in LDS and wave 0 finishes the head.  The kernel
-// streams W once (HBM-bound); a CU pulls the D x in_dim slice of one head.
-constexpr int kProjWaves = 16;
+// A workgroup owns one head vector (slot) of one token row, or 1/NSP of its
+// rows in split mode: its proj_waves(NSP) waves each compute RPW rows of W,
+// every lane accumulating 16-byte chunks of a row in f32 with x's matching
+// chunk (loaded once per chunk for all of the wave's rows), then a wave sum
+// per row.  The results meet in LDS and wave 0 finishes the head.  The
+// kernel streams W once (HBM-bound); a CU pulls the D x in_dim slice of one
+// head (a quarter of it in split mode).  Split mode runs 8 waves of D/32 rows
+// (x re-read by half as many waves: 10.8 against 11.1 us at the Qwen3-4B
+// decode shape); whole heads 16 waves of D/16 rows (the rows' loads in
+// flight stay within the register file at head_dim 256).
+constexpr int proj_waves(int nsp) { return nsp > 1 ? 8 : 16; }
 
 template <int WDT>
 struct WVec;
@@ -402,7 +406,7 @@ __device__ __forceinline__ void widen_w(const u32x4 &r, float *o) {
 }
 
 template <int D, int WDT, int QDT, int KVDT, int NSP>
-__global__ __launch_bounds__(kProjWaves * 64) void qkv_proj_kernel(
+__global__ __launch_bounds__(proj_waves(NSP) * 64) void qkv_proj_kernel(
     const float *__restrict__ x, int in_dim, const char *__restrict__ wq,
     const char *__restrict__ wk, const char *__restrict__ wv, const float *__restrict__ q_bias,
     const float *__restrict__ k_bias, const float *__restrict__ v_bias,
@@ -410,7 +414,7 @@ __global__ __launch_bounds__(kProjWaves * 64) void qkv_proj_kernel(
     const float *__restrict__ cs, int neox, int rotary_dim, int start_pos, int n_head,
     int n_kv_head, void *q_out, void *k_cache, void *v_cache, int64_t kv_stride,
     float *__restrict__ ws_y, uint32_t *__restrict__ ws_cnt) {
-    constexpr int E = D / 64, RPW = D / kProjWaves / NSP, VEC = WVec<WDT>::n;
+    constexpr int E = D / 64, RPW = D / proj_waves(NSP) / NSP, VEC = WVec<WDT>::n;
     constexpr int WB = WDT == ULLM_DT_F32 ? 4 : 2;  // bytes per weight
     static_assert(RPW >= 1, "rows per wave");
     __shared__ float ys[D];
@@ -706,7 +710,7 @@ static void launch_proj(bool split, int rows, hipStream_t st, const ProjArgs &a)
     auto go = [&](auto nspc) {
         constexpr int NSP = decltype(nspc)::value;
         hipLaunchKernelGGL((qkv_proj_kernel<D, WDT, QDT, KVDT, NSP>),
-                           dim3((unsigned)(slots * NSP), (unsigned)rows), dim3(kProjWaves * 64), 0, st,
+                           dim3((unsigned)(slots * NSP), (unsigned)rows), dim3(proj_waves(NSP) * 64), 0, st,
                            a.x, a.in_dim, a.wq, a.wk, a.wv, a.qb, a.kb, a.vb, a.qn, a.kn, a.eps, a.cs,
                            a.neox, a.rd, a.sp, a.nh, a.nkv, a.qo, a.kc, a.vc, a.kvs, a.ws_y, a.ws_cnt);
     };
