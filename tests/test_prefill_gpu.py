@@ -272,7 +272,7 @@ def test_f32_cache_geometries_covered():
 
 
 def test_cfg3_pipeline_norm_rope_all_rows(dev):
-    """cfg3 as BASELINE configures it, end to end at full size: raw f32 Q/K/V
+    """cfg3 as the benchmark configures it, end to end at full size: raw f32 Q/K/V
     ~ N(0,1) -> fused append (per-head RMSNorm with unit weights, eps 1e-6,
     NeoX RoPE theta 1e6, bf16 q and cache) -> causal prefill, every one of the
     2048 rows of all 32 heads against the oracle (lib.rs:1035-1058 then
