@@ -183,3 +183,30 @@ def test_paged_decode_random(dev, seed):
         ref = ora.attn_decode(qn[b].reshape(-1).copy(), k.float().numpy(), v.float().numpy(), n - 1,
                               H, Hk, D, 1.0 / math.sqrt(D), window=c["window"])
         assert_close(o[b].reshape(-1), ref, what=f"seed={seed} b={b}")
+
+
+def _append_case(seed):
+    rng = np.random.default_rng(5000 + seed)
+    H, Hk, D = _shape(rng)
+    if rng.integers(3) == 0:  # odd head counts leave partly empty head groups
+        Hk = int(rng.choice([1, 3, 5]))
+        H = Hk * int(rng.integers(1, 6))
+    rows = int(rng.choice([1, 2, 7, 64, 255, 256, 300]))
+    rd = D if rng.integers(2) else 2 * int(rng.integers(1, D // 2))
+    return dict(rows=rows, start_pos=int(rng.choice([0, 5, 1000])), H=H, Hk=Hk, D=D, rd=rd,
+                neox=bool(rng.integers(2)), norm=bool(rng.integers(2)), bias=bool(rng.integers(2)),
+                qdt=str(rng.choice(["f32", "f16", "bf16"])), kvdt=str(rng.choice(["f32", "f16", "bf16"])))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_append_random(dev, seed):
+    """Fused bias + Q/K norm + RoPE + cache store on random head counts,
+    head_dims, rotary widths, row counts (either side of the 256-row switch
+    between one workgroup per row and a row spread over workgroups) and
+    dtypes, against the oracle."""
+    from tests.test_append_gpu import run_case
+
+    c = _append_case(seed)
+    print(f"[append-rand] seed={seed} {c}", flush=True)
+    run_case(dev, c["rows"], c["start_pos"], c["H"], c["Hk"], c["D"], c["rd"], c["neox"],
+             norm=c["norm"], bias=c["bias"], qdt=c["qdt"], kvdt=c["kvdt"], seed=seed + 1)
