@@ -1,4 +1,5 @@
-"""Seeded random shapes for decode and prefill against the CPU oracle.
+"""Seeded random shapes for decode, prefill and the fused append against the
+CPU oracle.
 
 Each case draws head counts, GQA ratio, head_dim, dtype, lengths, start
 position, window and cache padding from a fixed seed, so the sweep covers
